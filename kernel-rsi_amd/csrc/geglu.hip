@@ -1,0 +1,226 @@
+// GEGLU forward and backward for gfx950 on a merged [a | b] GEMM output.
+//
+// Semantics follow library/geglu.py of the reference (kernel-rsi):
+//   _gelu_parts (geglu.py:20-24), tanh form:
+//     z = sqrt(2/pi) * (a + 0.044715 a^3);  t = 1 - 2 / (exp(2z) + 1);  gelu = 0.5 a (1 + t)
+//   forward  (_geglu_fwd, geglu.py:27-35):  out = bf16(gelu(a)) * b       (bf16 product)
+//   backward (_geglu_bwd, geglu.py:38-52):
+//     db   = g * bf16(gelu(a))                                            (bf16 product)
+//     dgel = float(bf16(g * b))
+//     da   = dgel * (0.5 (1 + t) + 0.5 a (1 - t^2) sqrt(2/pi) (1 + 3 * 0.044715 a^2))
+// The exact (erf) form, torch.nn.functional.gelu(approximate="none"), is
+//   gelu = 0.5 a (1 + erf(a / sqrt 2)),  gelu' = 0.5 (1 + erf(a / sqrt 2)) + a exp(-a^2 / 2) / sqrt(2 pi)
+// with the same bf16 rounding points.
+//
+// Design (MI355X): pure streaming. Each thread owns one 16-byte chunk of 8
+// columns of one row: one 128-bit load of a, one of b (and g), one or two
+// 128-bit stores; a workgroup covers 2048 contiguous columns of a row, so
+// every wave touches whole 1 KiB lines. The grid is 2-D (column tiles x row
+// slices) so no per-element division is needed. Non-multiple-of-8 widths or
+// unaligned pointers take a scalar element-per-thread path with the same math.
+#include "krsi_device.h"
+#include "krsi_internal.h"
+
+namespace krsi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr float kSqrt2OverPi = 0.7978845608028654f;
+constexpr float kKappa = 0.044715f;
+constexpr float kKappa3 = 0.134145f;  // 3 * 0.044715
+constexpr float kInvSqrt2 = 0.70710678118654752f;
+constexpr float kInvSqrt2Pi = 0.3989422804014327f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// tanh(z) = 1 - 2 / (e^{2z} + 1), the identity the reference uses; e^{2z}
+// overflows to +inf for large z and the quotient then gives exactly 1.
+__device__ __forceinline__ float tanh_via_exp(float z) {
+  const float e = __builtin_amdgcn_exp2f(2.0f * z * kLog2e);
+  return 1.0f - 2.0f / (e + 1.0f);
+}
+
+template <bool TANH>
+__device__ __forceinline__ float gelu_fwd(float a) {
+  if (TANH) {
+    const float z = kSqrt2OverPi * (a + kKappa * a * a * a);
+    return 0.5f * a * (1.0f + tanh_via_exp(z));
+  }
+  return 0.5f * a * (1.0f + erff(a * kInvSqrt2));
+}
+
+// Returns gelu(a) and writes gelu'(a) to d.
+template <bool TANH>
+__device__ __forceinline__ float gelu_fwd_bwd(float a, float& d) {
+  if (TANH) {
+    const float z = kSqrt2OverPi * (a + kKappa * a * a * a);
+    const float t = tanh_via_exp(z);
+    const float dz = kSqrt2OverPi * (1.0f + kKappa3 * a * a);
+    d = 0.5f * (1.0f + t) + 0.5f * a * (1.0f - t * t) * dz;
+    return 0.5f * a * (1.0f + t);
+  }
+  const float e = erff(a * kInvSqrt2);
+  const float pdf = __builtin_amdgcn_exp2f(-0.5f * a * a * kLog2e) * kInvSqrt2Pi;
+  d = 0.5f * (1.0f + e) + a * pdf;
+  return 0.5f * a * (1.0f + e);  // the forward's expression, so bf16(gelu) matches it
+}
+
+template <bool TANH>
+__global__ __launch_bounds__(kThreads) void geglu_fwd_vec(const uint16_t* __restrict__ u,
+                                                          uint16_t* __restrict__ out, int64_t rows,
+                                                          int f) {
+  const int f8 = f >> 3;
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= f8) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const u32x4* ur = reinterpret_cast<const u32x4*>(u + r * 2 * (int64_t)f);
+    const u32x4 av = ur[c], bv = ur[f8 + c];
+    float a[8], b[8], o[8];
+    unpack8(av, a);
+    unpack8(bv, b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = round_bf16(gelu_fwd<TANH>(a[j])) * b[j];
+    reinterpret_cast<u32x4*>(out + r * (int64_t)f)[c] = pack8(o);
+  }
+}
+
+template <bool TANH>
+__global__ __launch_bounds__(kThreads) void geglu_bwd_vec(const uint16_t* __restrict__ g,
+                                                          const uint16_t* __restrict__ u,
+                                                          uint16_t* __restrict__ du, int64_t rows,
+                                                          int f) {
+  const int f8 = f >> 3;
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= f8) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const u32x4* ur = reinterpret_cast<const u32x4*>(u + r * 2 * (int64_t)f);
+    const u32x4 av = ur[c], bv = ur[f8 + c];
+    const u32x4 gv = reinterpret_cast<const u32x4*>(g + r * (int64_t)f)[c];
+    float a[8], b[8], gg[8], da[8], db[8];
+    unpack8(av, a);
+    unpack8(bv, b);
+    unpack8(gv, gg);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float d;
+      const float gel = gelu_fwd_bwd<TANH>(a[j], d);
+      db[j] = gg[j] * round_bf16(gel);
+      const float dgel = round_bf16(gg[j] * b[j]);
+      da[j] = dgel * d;
+    }
+    u32x4* dr = reinterpret_cast<u32x4*>(du + r * 2 * (int64_t)f);
+    dr[c] = pack8(da);
+    dr[f8 + c] = pack8(db);
+  }
+}
+
+template <bool TANH>
+__global__ __launch_bounds__(kThreads) void geglu_fwd_scalar(const uint16_t* __restrict__ u,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t rows, int f) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= f) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const uint16_t* ur = u + r * 2 * (int64_t)f;
+    const float a = bf16_to_f32(ur[c]), b = bf16_to_f32(ur[f + c]);
+    out[r * (int64_t)f + c] = f32_to_bf16(round_bf16(gelu_fwd<TANH>(a)) * b);
+  }
+}
+
+template <bool TANH>
+__global__ __launch_bounds__(kThreads) void geglu_bwd_scalar(const uint16_t* __restrict__ g,
+                                                             const uint16_t* __restrict__ u,
+                                                             uint16_t* __restrict__ du,
+                                                             int64_t rows, int f) {
+  const int c = blockIdx.x * kThreads + threadIdx.x;
+  if (c >= f) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const uint16_t* ur = u + r * 2 * (int64_t)f;
+    const float a = bf16_to_f32(ur[c]), b = bf16_to_f32(ur[f + c]);
+    const float gg = bf16_to_f32(g[r * (int64_t)f + c]);
+    float d;
+    const float gel = gelu_fwd_bwd<TANH>(a, d);
+    uint16_t* dr = du + r * 2 * (int64_t)f;
+    dr[c] = f32_to_bf16(round_bf16(gg * b) * d);
+    dr[f + c] = f32_to_bf16(gg * round_bf16(gel));
+  }
+}
+
+// Grid: x = column tiles, y = row slices (<= 65535; rows beyond stride).
+dim3 grid_for(int64_t rows, int cols_per_thread_units) {
+  const int64_t gx = ceil_div(cols_per_thread_units, kThreads);
+  const int64_t gy = rows < 65535 ? rows : 65535;
+  return dim3((unsigned)gx, (unsigned)gy);
+}
+
+int check(int64_t rows, int32_t f, int32_t approximate) {
+  if (rows < 0 || f <= 0 || f > (1 << 28)) return KRSI_ERR_BAD_SHAPE;
+  if (approximate != 0 && approximate != 1) return KRSI_ERR_UNSUPPORTED;
+  return KRSI_OK;
+}
+
+}  // namespace
+}  // namespace krsi
+
+extern "C" {
+
+int krsi_geglu_fwd_bf16(const void* u, void* out, int64_t rows, int32_t f, int32_t approximate,
+                        void* stream) {
+  using namespace krsi;
+  int rc = check(rows, f, approximate);
+  if (rc != KRSI_OK) return rc;
+  if (rows == 0) return KRSI_OK;
+  if (!u || !out) return KRSI_ERR_NULL_POINTER;
+  hipStream_t st = as_stream(stream);
+  const bool vec = (f % 8 == 0) && aligned16(u) && aligned16(out);
+  const bool tanh_form = approximate == 1;
+  if (vec) {
+    const dim3 grid = grid_for(rows, f / 8);
+    if (tanh_form)
+      hipLaunchKernelGGL(geglu_fwd_vec<true>, grid, dim3(kThreads), 0, st, (const uint16_t*)u,
+                         (uint16_t*)out, rows, (int)f);
+    else
+      hipLaunchKernelGGL(geglu_fwd_vec<false>, grid, dim3(kThreads), 0, st, (const uint16_t*)u,
+                         (uint16_t*)out, rows, (int)f);
+  } else {
+    const dim3 grid = grid_for(rows, f);
+    if (tanh_form)
+      hipLaunchKernelGGL(geglu_fwd_scalar<true>, grid, dim3(kThreads), 0, st, (const uint16_t*)u,
+                         (uint16_t*)out, rows, (int)f);
+    else
+      hipLaunchKernelGGL(geglu_fwd_scalar<false>, grid, dim3(kThreads), 0, st, (const uint16_t*)u,
+                         (uint16_t*)out, rows, (int)f);
+  }
+  return launch_status();
+}
+
+int krsi_geglu_bwd_bf16(const void* g, const void* u, void* du, int64_t rows, int32_t f,
+                        int32_t approximate, void* stream) {
+  using namespace krsi;
+  int rc = check(rows, f, approximate);
+  if (rc != KRSI_OK) return rc;
+  if (rows == 0) return KRSI_OK;
+  if (!g || !u || !du) return KRSI_ERR_NULL_POINTER;
+  hipStream_t st = as_stream(stream);
+  const bool vec = (f % 8 == 0) && aligned16(g) && aligned16(u) && aligned16(du);
+  const bool tanh_form = approximate == 1;
+  if (vec) {
+    const dim3 grid = grid_for(rows, f / 8);
+    if (tanh_form)
+      hipLaunchKernelGGL(geglu_bwd_vec<true>, grid, dim3(kThreads), 0, st, (const uint16_t*)g,
+                         (const uint16_t*)u, (uint16_t*)du, rows, (int)f);
+    else
+      hipLaunchKernelGGL(geglu_bwd_vec<false>, grid, dim3(kThreads), 0, st, (const uint16_t*)g,
+                         (const uint16_t*)u, (uint16_t*)du, rows, (int)f);
+  } else {
+    const dim3 grid = grid_for(rows, f);
+    if (tanh_form)
+      hipLaunchKernelGGL(geglu_bwd_scalar<true>, grid, dim3(kThreads), 0, st, (const uint16_t*)g,
+                         (const uint16_t*)u, (uint16_t*)du, rows, (int)f);
+    else
+      hipLaunchKernelGGL(geglu_bwd_scalar<false>, grid, dim3(kThreads), 0, st, (const uint16_t*)g,
+                         (const uint16_t*)u, (uint16_t*)du, rows, (int)f);
+  }
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,72 @@
+// Device-side helpers shared by the gfx950 kernels: bf16 <-> fp32 conversion,
+// 128-bit vector types, wave64 reductions and the bf16 MFMA wrapper.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace krsi {
+
+constexpr int kWave = 64;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// bf16 is stored as raw 16-bit patterns. Widening is exact: the bf16 bits are
+// the top half of the fp32 bits.
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16 with round-to-nearest-even (gfx950 v_cvt_pk_bf16_f32), the
+// rounding torch uses for .to(torch.bfloat16).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+// Round fp32 to the nearest bf16 and widen back: the value a bf16 tensor
+// would hold at this point of an eager computation.
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Unpack 8 bf16 (one 128-bit word) to fp32.
+__device__ __forceinline__ void unpack8(const u32x4& w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf_lo(w[i]);
+    f[2 * i + 1] = bf_hi(w[i]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return w;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// D = A(32x16) * B(16x32) + C on bf16 MFMA, fp32 accumulate.
+// Operand convention used by every kernel in this library (wave64):
+//   A: lane l holds A[m = l % 32][k = 8 * (l / 32) + j], j = 0..7
+//   B: lane l holds B[k = 8 * (l / 32) + j][n = l % 32], j = 0..7
+//   D: lane l, register r holds D[m = 8 * (r / 4) + 4 * (l / 32) + r % 4][n = l % 32]
+// Only the pairing of A and B slots matters for K (it is summed over), so a
+// kernel may assign any logical K index to (l / 32, j) as long as A and B agree.
+__device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+}  // namespace krsi

@@ -1,0 +1,759 @@
+// Relative-position-bias flash attention (non-causal), forward and backward,
+// for gfx950 on bf16 MFMA (v_mfma_f32_32x32x16_bf16), fp32 softmax.
+//
+// Semantics follow library/relpos_attention.py of the reference (kernel-rsi):
+//   s[i,j]   = (q_i . k_j * scale + pd[h, j - i + S - 1]) * log2(e)     (:46)
+//   forward  : online softmax over key blocks with exp2, o = sum_j bf16(p_ij) v_j / l_i,
+//              stored as bf16 and fp32, lse_i = m_i + log2(l_i)             (:26-59)
+//   backward : delta_i = sum_d dO_id * O32_id                                (:144)
+//              p = exp2(s - lse), dp = dO v^T, ds = p (dp - delta)          (:86-90, :121-124)
+//              dV = bf16(p)^T dO, dK = scale * bf16(ds)^T q,
+//              dQ = scale * bf16(ds) k                                       (:88-94, :125-126)
+//              dpd[h, k] = sum over b, i, j with j - i + S - 1 = k of ds     (:154-156)
+//
+// Layout and tiling (MI355X-native, not the reference's):
+//   * Wave64 owns 32 queries (forward, dQ) or 32 keys (dK/dV); a workgroup of
+//     4 waves owns 128. The register-resident side (Q and dO, or K and V) is
+//     loaded once as MFMA B operands straight from HBM with 128-bit loads.
+//   * The streamed side is staged per iteration in LDS, row-major for the
+//     products that contract over the head dim and transposed (head dim x
+//     position, 8-row XOR swizzle) for the products that contract over
+//     positions. Global loads of iteration t+1 are issued before the MFMAs of
+//     iteration t (register double buffering).
+//   * Scores are computed transposed (S^T = K Q^T) in the forward and dQ
+//     kernels, so each lane owns one query: row max and row sum are in-lane
+//     reductions plus one cross-half exchange, and lse/delta are registers.
+//     The fp32 score tile is converted in place to the B operand of the next
+//     MFMA; the K-dimension permutation this implies is mirrored in the LDS
+//     layout of the other operand (perm_pos).
+//   * The Toeplitz bias is staged once per iteration as a window of
+//     BM + BN - 1 entries (times log2 e), in 4 copies shifted by one element,
+//     so every lane fetches its 4 consecutive entries with one aligned 128-bit
+//     LDS read.
+//   * Online softmax keeps the exact running max per 64-key block (so the
+//     block maximum gives p = 1, exact in bf16, as in the reference); the
+//     fp32 accumulators are rescaled only when some lane's max moved.
+//   * dpd is reduced along the diagonals j - i inside the dQ kernel: each
+//     (wave, half-wave) adds its fp32 ds into a private 256-entry LDS ring
+//     indexed by diagonal (collision-free, so a plain read-modify-write in
+//     program order is exact and deterministic), the
+//     finished diagonals are folded in a fixed order into one partial row per
+//     128-query block, and a last kernel sums the partial rows over batch and
+//     query blocks in a fixed order. No [B, H, S, S] buffer exists.
+#include <math.h>
+
+#include "krsi_device.h"
+#include "krsi_internal.h"
+
+namespace krsi {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRows = 128;     // queries (forward, dQ) or keys (dK/dV) per workgroup
+constexpr int kStep = 64;      // streamed positions per iteration
+constexpr int kTLD = kStep + 8;            // transposed tile row stride (bf16)
+constexpr int kWin = kRows + kStep - 1;    // bias window entries
+constexpr int kWLD = 196;                  // bias copy length (>= kWin + 3, multiple of 4)
+constexpr int kRing = 256;                 // dpd ring entries per (wave, half)
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int DP>
+struct Geo {
+  static constexpr int KS = DP / 16;         // K steps of 16 over the head dim
+  static constexpr int DB = (DP + 31) / 32;  // 32-wide head-dim blocks of head-dim outputs
+  static constexpr int DPV = DB * 32;
+  static constexpr int KLD = DP + 8;         // row-major tile stride (bf16)
+  static constexpr int CPR = DP / 8;         // 16-byte chunks per row
+  static constexpr int NCH = kStep * CPR;    // chunks per streamed tile
+  static constexpr int CPT = (NCH + kThreads - 1) / kThreads;
+};
+
+constexpr int kBPT = (4 * kWLD + kThreads - 1) / kThreads;  // bias entries per thread
+
+// Position of streamed element `pos` (0..63) in a transposed tile row `d`.
+// Bits 2 and 3 are swapped so that the 8 positions a lane needs for one MFMA
+// step are contiguous (the K order of an fp32 D tile reused as a bf16
+// operand: registers 8u..8u+7 of half g hold positions 16u + 4g + {0..3} and
+// 16u + 8 + 4g + {0..3}); bits 3..5 are XORed with (d / 8) % 8 so that the
+// transposing 16-bit writes of 8 consecutive head-dim rows hit 8 banks.
+__device__ __forceinline__ int perm_pos(int d, int pos) {
+  const int p = (pos & ~12) | ((pos >> 1) & 4) | ((pos << 1) & 8);
+  return p ^ (((d >> 3) & 7) << 3);
+}
+
+// Start of the 8 contiguous positions holding MFMA step `base` (a multiple of
+// 8 before permutation) for head-dim row d.
+__device__ __forceinline__ int perm_base(int d, int base) { return base ^ (((d >> 3) & 7) << 3); }
+
+__device__ __forceinline__ uint16_t elem16(const u32x4& v, int e) {
+  return (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
+}
+
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+constexpr u32x4 kZero4 = {0u, 0u, 0u, 0u};
+
+// Stage one streamed tile of kStep rows x DP columns: row-major into `rm`
+// (may be null) and transposed into `tr` (may be null).
+template <int DP>
+__device__ __forceinline__ void stash_tile(const u32x4* regs, uint16_t* rm, uint16_t* tr) {
+  using G = Geo<DP>;
+#pragma unroll
+  for (int k = 0; k < G::CPT; ++k) {
+    const int c = threadIdx.x + k * kThreads;
+    if (c < G::NCH) {
+      const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
+      if (rm) *reinterpret_cast<u32x4*>(rm + row * G::KLD + d0) = regs[k];
+      if (tr) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tr[(d0 + e) * kTLD + perm_pos(d0 + e, row)] = elem16(regs[k], e);
+      }
+    }
+  }
+}
+
+// Load one streamed tile (rows p0..p0+63 of a [*, ld] bf16 matrix whose
+// column block starts at `col`) into registers, zero outside [0, S) x [0, D).
+template <int DP>
+__device__ __forceinline__ void load_tile(u32x4* regs, const uint16_t* col, int64_t ld, int64_t tok0,
+                                          int p0, int S, int D) {
+  using G = Geo<DP>;
+#pragma unroll
+  for (int k = 0; k < G::CPT; ++k) {
+    const int c = threadIdx.x + k * kThreads;
+    const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
+    const bool ok = c < G::NCH && p0 + row < S && d0 < D;
+    regs[k] = ok ? ld16(col + (tok0 + p0 + row) * ld + d0) : kZero4;
+  }
+}
+
+// Bias window: copy cc, position y holds T[wb + sgn * (y - cc)] * log2(e),
+// zero outside [0, 2S - 1).
+__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn) {
+#pragma unroll
+  for (int k = 0; k < kBPT; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    const int cc = e / kWLD, y = e - cc * kWLD;
+    const int src = wb + sgn * (y - cc);
+    regs[k] = (e < 4 * kWLD && src >= 0 && src < npd) ? pdh[src] * kLog2e : 0.f;
+  }
+}
+
+__device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
+#pragma unroll
+  for (int k = 0; k < kBPT; ++k) {
+    const int e = threadIdx.x + k * kThreads;
+    if (e < 4 * kWLD) bw[e] = regs[k];
+  }
+}
+
+// The 16 bias values of one 32x32 D tile: entries x0 + 8a + b (a, b = 0..3)
+// of the window, read from the copy that makes x0 16-byte aligned.
+__device__ __forceinline__ void read_bias16(const float* bw, int x0, float* out) {
+  const int cc = (-x0) & 3;
+  const float* p = bw + cc * kWLD + x0 + cc;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 8 * a);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) out[4 * a + b] = v[b];
+  }
+}
+
+// ------------------------------------------------------------------- forward
+template <int DP>
+__global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
+    int D, float c) {
+  using G = Geo<DP>;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[G::DPV * kTLD];
+  __shared__ __attribute__((aligned(16))) float Bw[4 * kWLD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  const int i_wg = blockIdx.x * kRows;
+  const int ii = wave * 32 + l32;
+  const int qi = i_wg + ii;
+  const bool qvalid = qi < S;
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t HD = (int64_t)H * D;
+  const uint16_t* qcol = qkv + (int64_t)h * D;
+  const uint16_t* kcol = qkv + HD + (int64_t)h * D;
+  const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
+  const int npd = 2 * S - 1;
+  const float* pdh = pd + (int64_t)h * npd;
+
+  for (int e = tid; e < (G::DPV - DP) * kTLD; e += kThreads) Vt[DP * kTLD + e] = 0;
+
+  u32x4 qreg[G::KS];
+#pragma unroll
+  for (int s = 0; s < G::KS; ++s) {
+    const int d0 = 16 * s + 8 * g;
+    qreg[s] = (qvalid && d0 < D) ? ld16(qcol + (tok0 + qi) * ld + d0) : kZero4;
+  }
+
+  f32x16 oacc[G::DB];
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  u32x4 kst[G::CPT], vst[G::CPT];
+  float bst[kBPT];
+  const int T = (S + kStep - 1) / kStep;
+  load_tile<DP>(kst, kcol, ld, tok0, 0, S, D);
+  load_tile<DP>(vst, vcol, ld, tok0, 0, S, D);
+  load_bias(bst, pdh, npd, 0 - i_wg - (kRows - 1) + S - 1, 1);
+
+  for (int t = 0; t < T; ++t) {
+    const int j0 = t * kStep;
+    __syncthreads();
+    stash_tile<DP>(kst, Ks, nullptr);
+    stash_tile<DP>(vst, nullptr, Vt);
+    stash_bias(bst, Bw);
+    __syncthreads();
+    if (t + 1 < T) {
+      load_tile<DP>(kst, kcol, ld, tok0, j0 + kStep, S, D);
+      load_tile<DP>(vst, vcol, ld, tok0, j0 + kStep, S, D);
+      load_bias(bst, pdh, npd, j0 + kStep - i_wg - (kRows - 1) + S - 1, 1);
+    }
+
+    float sc[2][16];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < G::KS; ++s)
+        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::KLD + 16 * s + 8 * g), qreg[s], acc);
+      float bias[16];
+      read_bias16(Bw, kb * 32 + 4 * g + (kRows - 1) - ii, bias);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[kb][r] = acc[r] * c + bias[r];
+    }
+    if (j0 + kStep > S) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sc[kb][r] = -INFINITY;
+    }
+    float mx = sc[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // Exact running max, as the reference (relpos_attention.py:48-50): the block's largest
+    // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
+    // some lane's max moved.
+    const bool need = mx > m_run;
+    if (__any(need)) {
+      const float mnew = need ? mx : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      m_run = mnew;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(sc[kb][r] - m_run);
+        l_run += p;
+        sc[kb][r] = p;
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4 pb = pack8(&sc[kb][8 * u]);
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+          const int d = db * 32 + l32;
+          oacc[db] = mfma32x32x16(ld16(Vt + d * kTLD + perm_base(d, kb * 32 + 16 * u + 8 * g)), pb,
+                                  oacc[db]);
+        }
+      }
+  }
+
+  const float l = l_run + __shfl_xor(l_run, 32);
+  if (qvalid) {
+    const int64_t obase = (tok0 + qi) * HD + (int64_t)h * D;
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int d0 = db * 32 + 8 * a + 4 * g;
+        if (d0 < D) {
+          f32x4 o;
+#pragma unroll
+          for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
+          *reinterpret_cast<f32x4*>(out32 + obase + d0) = o;
+          uint2 ob;
+          ob.x = pack_bf16x2(o[0], o[1]);
+          ob.y = pack_bf16x2(o[2], o[3]);
+          *reinterpret_cast<uint2*>(out + obase + d0) = ob;
+        }
+      }
+    if (g == 0) lse[(int64_t)bh * S + qi] = m_run + log2f(l);
+  }
+}
+
+// ------------------------------------------------ backward: delta, dQ and dpd
+template <int DP>
+__global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    const uint16_t* __restrict__ dout, const float* __restrict__ out32,
+    const float* __restrict__ lse, float* __restrict__ delta_ws, float* __restrict__ part,
+    uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H, int D, float c, float scale) {
+  using G = Geo<DP>;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[G::DPV * kTLD];
+  __shared__ __attribute__((aligned(16))) float Bw[4 * kWLD];
+  __shared__ float ring[8][kRing];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  const int i_wg = blockIdx.x * kRows;
+  const int ii = wave * 32 + l32;
+  const int qi = i_wg + ii;
+  const bool qvalid = qi < S;
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t HD = (int64_t)H * D;
+  const uint16_t* qcol = qkv + (int64_t)h * D;
+  const uint16_t* kcol = qkv + HD + (int64_t)h * D;
+  const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
+  const int npd = 2 * S - 1;
+  const float* pdh = pd + (int64_t)h * npd;
+  const int RS = S + 128;  // partial row stride
+  const int rlen = S + kRows - 1;
+  float* prow = part + ((int64_t)bh * gridDim.x + blockIdx.x) * RS;
+
+  for (int e = tid; e < (G::DPV - DP) * kTLD; e += kThreads) Kt[DP * kTLD + e] = 0;
+  for (int e = tid; e < 8 * kRing; e += kThreads) (&ring[0][0])[e] = 0.f;
+
+  // Register-resident operands and per-query statistics.
+  u32x4 qreg[G::KS], doreg[G::KS];
+  float dsum = 0.f;
+  const int64_t obase = (tok0 + qi) * HD + (int64_t)h * D;
+#pragma unroll
+  for (int s = 0; s < G::KS; ++s) {
+    const int d0 = 16 * s + 8 * g;
+    const bool ok = qvalid && d0 < D;
+    qreg[s] = ok ? ld16(qcol + (tok0 + qi) * ld + d0) : kZero4;
+    doreg[s] = ok ? ld16(dout + obase + d0) : kZero4;
+    if (ok) {
+      const f32x4 o0 = *reinterpret_cast<const f32x4*>(out32 + obase + d0);
+      const f32x4 o1 = *reinterpret_cast<const f32x4*>(out32 + obase + d0 + 4);
+      float df[8];
+      unpack8(doreg[s], df);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dsum += df[e] * o0[e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dsum += df[4 + e] * o1[e];
+    }
+  }
+  const float delta = dsum + __shfl_xor(dsum, 32);
+  const float lse_q = qvalid ? lse[(int64_t)bh * S + qi] : 0.f;
+  if (qvalid && g == 0) delta_ws[(int64_t)bh * S + qi] = delta;
+
+  f32x16 dq[G::DB];
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
+
+  float* myring = ring[wave * 2 + g];
+  u32x4 kst[G::CPT], vst[G::CPT];
+  float bst[kBPT];
+  const int T = (S + kStep - 1) / kStep;
+  load_tile<DP>(kst, kcol, ld, tok0, 0, S, D);
+  load_tile<DP>(vst, vcol, ld, tok0, 0, S, D);
+  load_bias(bst, pdh, npd, 0 - i_wg - (kRows - 1) + S - 1, 1);
+
+  for (int t = 0; t < T; ++t) {
+    const int j0 = t * kStep;
+    __syncthreads();
+    stash_tile<DP>(kst, Ks, Kt);
+    stash_tile<DP>(vst, Vs, nullptr);
+    stash_bias(bst, Bw);
+    __syncthreads();
+    if (t + 1 < T) {
+      load_tile<DP>(kst, kcol, ld, tok0, j0 + kStep, S, D);
+      load_tile<DP>(vst, vcol, ld, tok0, j0 + kStep, S, D);
+      load_bias(bst, pdh, npd, j0 + kStep - i_wg - (kRows - 1) + S - 1, 1);
+    }
+    // Diagonals r in [64(t-1), 64t) received their last contribution in
+    // iteration t-1: fold the 8 rings in order into the partial row.
+    if (t > 0 && wave == 0) {
+      const int r = (t - 1) * kStep + lane;
+      const int slot = r & (kRing - 1);
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        v += ring[k][slot];
+        ring[k][slot] = 0.f;
+      }
+      prow[r] = v;
+    }
+
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16 acc, accp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < G::KS; ++s) {
+        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::KLD + 16 * s + 8 * g), qreg[s], acc);
+        accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::KLD + 16 * s + 8 * g), doreg[s], accp);
+      }
+      float bias[16];
+      const int x0 = kb * 32 + 4 * g + (kRows - 1) - ii;
+      read_bias16(Bw, x0, bias);
+      const bool tail = j0 + kStep > S;
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - lse_q);
+        if (!qvalid) p = 0.f;
+        if (tail && j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
+        ds[r] = p * (accp[r] - delta);
+      }
+      // Diagonal of D-register r: j - i + 127 - i_wg = 64t + x0 + 8a + b. Within one
+      // register the 32 lanes of a half hit 32 distinct slots of their own ring, and LDS
+      // operations of a wave complete in order, so a plain read-modify-write is exact
+      // (LDS float atomics cost ~30x more here).
+#pragma unroll
+      for (int r = 0; r < 16; ++r) myring[(j0 + x0 + 8 * (r >> 2) + (r & 3)) & (kRing - 1)] += ds[r];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4 dsb = pack8(&ds[8 * u]);
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+          const int d = db * 32 + l32;
+          dq[db] = mfma32x32x16(ld16(Kt + d * kTLD + perm_base(d, kb * 32 + 16 * u + 8 * g)), dsb,
+                                dq[db]);
+        }
+      }
+    }
+  }
+
+  __syncthreads();
+  for (int r = (T - 1) * kStep + tid; r < rlen; r += kThreads) {
+    const int slot = r & (kRing - 1);
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v += ring[k][slot];
+    prow[r] = v;
+  }
+
+  if (qvalid) {
+    const int64_t qbase = (tok0 + qi) * ldd + (int64_t)h * D;
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int d0 = db * 32 + 8 * a + 4 * g;
+        if (d0 < D) {
+          uint2 ob;
+          ob.x = pack_bf16x2(dq[db][4 * a] * scale, dq[db][4 * a + 1] * scale);
+          ob.y = pack_bf16x2(dq[db][4 * a + 2] * scale, dq[db][4 * a + 3] * scale);
+          *reinterpret_cast<uint2*>(dqkv + qbase + d0) = ob;
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------- backward: dK, dV
+template <int DP>
+__global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H,
+    int D, float c, float scale) {
+  using G = Geo<DP>;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[kStep * G::KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Qt[G::DPV * kTLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Os[kStep * G::KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ot[G::DPV * kTLD];
+  __shared__ __attribute__((aligned(16))) float Lq[kStep];
+  __shared__ __attribute__((aligned(16))) float Dq[kStep];
+  __shared__ __attribute__((aligned(16))) float Bw[4 * kWLD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  const int j_wg = blockIdx.x * kRows;
+  const int kk = wave * 32 + l32;
+  const int kj = j_wg + kk;
+  const bool kvalid = kj < S;
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t HD = (int64_t)H * D;
+  const uint16_t* qcol = qkv + (int64_t)h * D;
+  const uint16_t* kcol = qkv + HD + (int64_t)h * D;
+  const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
+  const uint16_t* ocol = dout + (int64_t)h * D;
+  const int npd = 2 * S - 1;
+  const float* pdh = pd + (int64_t)h * npd;
+  const float* lse_bh = lse + (int64_t)bh * S;
+  const float* dl_bh = delta_ws + (int64_t)bh * S;
+
+  for (int e = tid; e < (G::DPV - DP) * kTLD; e += kThreads) {
+    Qt[DP * kTLD + e] = 0;
+    Ot[DP * kTLD + e] = 0;
+  }
+
+  u32x4 kreg[G::KS], vreg[G::KS];
+#pragma unroll
+  for (int s = 0; s < G::KS; ++s) {
+    const int d0 = 16 * s + 8 * g;
+    const bool ok = kvalid && d0 < D;
+    kreg[s] = ok ? ld16(kcol + (tok0 + kj) * ld + d0) : kZero4;
+    vreg[s] = ok ? ld16(vcol + (tok0 + kj) * ld + d0) : kZero4;
+  }
+
+  f32x16 dk[G::DB], dv[G::DB];
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+
+  u32x4 qst[G::CPT], ost[G::CPT];
+  float bst[kBPT];
+  float sst = 0.f;
+  const int T = (S + kStep - 1) / kStep;
+  // Reversed window: copy cc, position y holds T[rb - (y - cc)], rb the
+  // largest diagonal of the iteration.
+  auto stats = [&](int i0) {
+    const int q = i0 + (tid & 63);
+    if (tid < 128) sst = q < S ? (tid < 64 ? lse_bh[q] : dl_bh[q]) : 0.f;
+  };
+  load_tile<DP>(qst, qcol, ld, tok0, 0, S, D);
+  load_tile<DP>(ost, ocol, HD, tok0, 0, S, D);
+  load_bias(bst, pdh, npd, (j_wg + kRows - 1) - 0 + S - 1, -1);
+  stats(0);
+
+  for (int t = 0; t < T; ++t) {
+    const int i0 = t * kStep;
+    __syncthreads();
+    stash_tile<DP>(qst, Qs, Qt);
+    stash_tile<DP>(ost, Os, Ot);
+    stash_bias(bst, Bw);
+    if (tid < 64) Lq[tid] = sst;
+    else if (tid < 128) Dq[tid - 64] = sst;
+    __syncthreads();
+    if (t + 1 < T) {
+      load_tile<DP>(qst, qcol, ld, tok0, i0 + kStep, S, D);
+      load_tile<DP>(ost, ocol, HD, tok0, i0 + kStep, S, D);
+      load_bias(bst, pdh, npd, (j_wg + kRows - 1) - (i0 + kStep) + S - 1, -1);
+      stats(i0 + kStep);
+    }
+    const bool tail = i0 + kStep > S;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      f32x16 acc, accp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < G::KS; ++s) {
+        acc = mfma32x32x16(ld16(Qs + (qb * 32 + l32) * G::KLD + 16 * s + 8 * g), kreg[s], acc);
+        accp = mfma32x32x16(ld16(Os + (qb * 32 + l32) * G::KLD + 16 * s + 8 * g), vreg[s], accp);
+      }
+      float bias[16];
+      read_bias16(Bw, (kRows - 1) - kk + qb * 32 + 4 * g, bias);
+      float p[16], ds[16];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(Lq + qb * 32 + 8 * a + 4 * g);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dq + qb * 32 + 8 * a + 4 * g);
+#pragma unroll
+        for (int b4 = 0; b4 < 4; ++b4) {
+          const int r = 4 * a + b4;
+          float pv = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - l4[b4]);
+          if (tail && i0 + qb * 32 + 8 * a + 4 * g + b4 >= S) pv = 0.f;
+          p[r] = pv;
+          ds[r] = pv * (accp[r] - d4[b4]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4 pa = pack8(&p[8 * u]);
+        const u32x4 dsa = pack8(&ds[8 * u]);
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+          const int d = db * 32 + l32;
+          const int off = d * kTLD + perm_base(d, qb * 32 + 16 * u + 8 * g);
+          dv[db] = mfma32x32x16(pa, ld16(Ot + off), dv[db]);
+          dk[db] = mfma32x32x16(dsa, ld16(Qt + off), dk[db]);
+        }
+      }
+    }
+  }
+
+  // D layout: lane = head dim d (n), register r = key 8(r/4) + 4g + r%4 of this wave.
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db) {
+    const int d = db * 32 + l32;
+    if (d < D) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = j_wg + wave * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key < S) {
+          uint16_t* rowp = dqkv + (tok0 + key) * ldd + HD + (int64_t)h * D + d;
+          rowp[0] = f32_to_bf16(dk[db][r] * scale);
+          rowp[HD] = f32_to_bf16(dv[db][r]);
+        }
+      }
+    }
+  }
+}
+
+// dpd[h, k] = sum over b and 128-query blocks of the partial rows, fixed order.
+// Block: 64 diagonals (lane) of head h; the 4 waves take every 4th (b, query
+// block) term, then the 4 wave sums are added in wave order.
+__global__ __launch_bounds__(kThreads) void relpos_dpd_reduce(const float* __restrict__ part,
+                                                              float* __restrict__ dpd, int B, int S,
+                                                              int H, int nqb) {
+  __shared__ float s[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + lane;
+  const int h = blockIdx.y;
+  const int npd = 2 * S - 1;
+  const int RS = S + 128;
+  const int rlen = S + kRows - 1;
+  float acc = 0.f;
+  if (k < npd) {
+    const int terms = B * nqb;
+#pragma unroll 4
+    for (int e = wave; e < terms; e += 4) {
+      const int b = e / nqb, qb = e - b * nqb;
+      const int r = k - S + 128 + kRows * qb;
+      if (r >= 0 && r < rlen) acc += part[((int64_t)(b * H + h) * nqb + qb) * RS + r];
+    }
+  }
+  s[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && k < npd) dpd[(int64_t)h * npd + k] = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
+}
+
+int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float scale) {
+  if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return KRSI_ERR_BAD_SHAPE;
+  if (D % 8 != 0 || D > 128) return KRSI_ERR_UNSUPPORTED;
+  if ((int64_t)B * H > 65535 || S > (1 << 24)) return KRSI_ERR_BAD_SHAPE;
+  if (ld < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
+  if (ld % 8 != 0 || !aligned16(qkv)) return KRSI_ERR_MISALIGNED;
+  if (!(scale == scale) || scale > 3.0e38f || scale < -3.0e38f) return KRSI_ERR_BAD_SCALE;
+  return KRSI_OK;
+}
+
+int padded_dim(int D) { return (D + 15) / 16 * 16; }
+
+size_t ws_delta_bytes(int B, int S, int H) { return align256((size_t)B * H * S * sizeof(float)); }
+size_t ws_part_bytes(int B, int S, int H) {
+  const size_t nqb = (size_t)ceil_div(S, kRows);
+  return align256((size_t)B * H * nqb * (size_t)(S + 128) * sizeof(float));
+}
+
+template <int DP>
+void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* out32, float* lse,
+                int B, int S, int H, int D, float c, hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(S, kRows), (unsigned)(B * H));
+  hipLaunchKernelGGL(relpos_fwd_kernel<DP>, grid, dim3(kThreads), 0, st, (const uint16_t*)qkv, ld,
+                     pd, (uint16_t*)out, out32, lse, S, H, D, c);
+}
+
+template <int DP>
+void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
+                const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S, int H,
+                int D, float c, float scale, hipStream_t st) {
+  float* delta = static_cast<float*>(ws);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_delta_bytes(B, S, H));
+  const int nqb = (int)ceil_div(S, kRows);
+  const dim3 grid((unsigned)nqb, (unsigned)(B * H));
+  hipLaunchKernelGGL(relpos_bwd_dq_kernel<DP>, grid, dim3(kThreads), 0, st, (const uint16_t*)qkv,
+                     ld, pd, (const uint16_t*)dout, out32, lse, delta, part, (uint16_t*)dqkv, ldd,
+                     S, H, D, c, scale);
+  hipLaunchKernelGGL(relpos_bwd_dkdv_kernel<DP>, grid, dim3(kThreads), 0, st,
+                     (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
+                     (const float*)delta, (uint16_t*)dqkv, ldd, S, H, D, c, scale);
+  const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
+  hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(kThreads), 0, st, (const float*)part, dpd, B,
+                     S, H, nqb);
+}
+
+}  // namespace
+}  // namespace krsi
+
+extern "C" {
+
+int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void* out, float* out32,
+                         float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
+                         void* stream) {
+  using namespace krsi;
+  if (!qkv || !pd || !out || !out32 || !lse) return KRSI_ERR_NULL_POINTER;
+  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
+  if (rc != KRSI_OK) return rc;
+  if (!aligned16(out) || !aligned16(out32)) return KRSI_ERR_MISALIGNED;
+  const float c = scale * kLog2e;
+  hipStream_t st = as_stream(stream);
+  switch (padded_dim(D)) {
+#define KRSI_CASE(DPV_)                                                                \
+  case DPV_:                                                                           \
+    launch_fwd<DPV_>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, c, st);             \
+    break;
+    KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
+    KRSI_CASE(112) KRSI_CASE(128)
+#undef KRSI_CASE
+    default:
+      return KRSI_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t D) {
+  using namespace krsi;
+  (void)D;
+  if (B <= 0 || S <= 0 || H <= 0) return 0;
+  return ws_delta_bytes(B, S, H) + ws_part_bytes(B, S, H);
+}
+
+int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
+                         const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv,
+                         float* dpd, void* workspace, size_t workspace_bytes, int32_t B, int32_t S,
+                         int32_t H, int32_t D, float scale, void* stream) {
+  using namespace krsi;
+  if (!dout || !qkv || !pd || !out32 || !lse || !dqkv || !dpd) return KRSI_ERR_NULL_POINTER;
+  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
+  if (rc != KRSI_OK) return rc;
+  if (ld_dqkv < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
+  if (ld_dqkv % 8 != 0 || !aligned16(dqkv) || !aligned16(dout) || !aligned16(out32))
+    return KRSI_ERR_MISALIGNED;
+  if (!workspace || workspace_bytes < krsi_relpos_bwd_workspace_bytes(B, S, H, D))
+    return KRSI_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return KRSI_ERR_MISALIGNED;
+  const float c = scale * kLog2e;
+  hipStream_t st = as_stream(stream);
+  switch (padded_dim(D)) {
+#define KRSI_CASE(DPV_)                                                                      \
+  case DPV_:                                                                                 \
+    launch_bwd<DPV_>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace, B, S, \
+                     H, D, c, scale, st);                                                    \
+    break;
+    KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
+    KRSI_CASE(112) KRSI_CASE(128)
+#undef KRSI_CASE
+    default:
+      return KRSI_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+}  // extern "C"

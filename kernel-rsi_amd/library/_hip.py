@@ -1,0 +1,217 @@
+"""ctypes binding of libkrsi_hip.so (the C ABI declared in include/krsi.h) and the
+host wrappers that validate tensors, allocate outputs and workspaces with the
+torch caching allocator, and launch on torch's current stream.
+
+There is no CPU or torch fallback: a call without the built library, or with
+tensors that are not on a GPU, raises. The library is loaded lazily, after
+torch, so that it binds to the HIP runtime torch has already loaded.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+ABI_VERSION = 1
+LIB_PATH = Path(__file__).resolve().parent.parent / "libkrsi_hip.so"
+
+# Names and signatures of every entry point of include/krsi.h.
+_P, _I32, _I64, _F32, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+SIGNATURES = {
+    "krsi_abi_version": (ctypes.c_int, []),
+    "krsi_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "krsi_rmsnorm_fwd_bf16": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _F32, _P]),
+    "krsi_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I32]),
+    "krsi_rmsnorm_bwd_bf16": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I32, _P]),
+    "krsi_geglu_fwd_bf16": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P]),
+    "krsi_geglu_bwd_bf16": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P]),
+    "krsi_relpos_fwd_bf16": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _P]),
+    "krsi_relpos_bwd_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "krsi_relpos_bwd_bf16": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _SZ,
+                                            _I32, _I32, _I32, _I32, _F32, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class KrsiError(RuntimeError):
+    """A nonzero status from libkrsi_hip.so."""
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded and checked on first use)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.is_file():
+                    raise ImportError(f"{LIB_PATH} is not built; run `python kernel-rsi_amd/build.py` "
+                                      "(or __graft_entry__.build()) first")
+                handle = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype, fn.argtypes = res, args
+                if handle.krsi_abi_version() != ABI_VERSION:
+                    raise ImportError(f"{LIB_PATH}: ABI version {handle.krsi_abi_version()} != {ABI_VERSION}")
+                _lib = handle
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise KrsiError(lib().krsi_error_string(rc).decode())
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise ValueError("krsi kernels run on the GPU only: got a tensor on "
+                             f"{t.device} (there is no CPU path)")
+    dev = ts[0].device
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+
+
+def _bf16(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be torch.bfloat16, got {t.dtype}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ------------------------------------------------------------------- RMSNorm
+def rmsnorm_fwd(x2d: torch.Tensor, w: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """y, rstd for a contiguous [rows, N] bf16 x2d and [N] bf16 weight."""
+    _on_gpu(x2d, w)
+    _bf16("x2d", x2d)
+    _bf16("weight", w)
+    if x2d.dim() != 2 or not x2d.is_contiguous():
+        raise ValueError("x2d must be a contiguous 2D tensor [rows, N]")
+    rows, n = x2d.shape
+    if w.shape != (n,):
+        raise ValueError(f"weight shape {tuple(w.shape)} != ({n},)")
+    w = w.contiguous()
+    y = torch.empty_like(x2d)
+    rstd = torch.empty(rows, device=x2d.device, dtype=torch.float32)
+    if rows:
+        _check(lib().krsi_rmsnorm_fwd_bf16(_ptr(x2d), _ptr(w), _ptr(y), _ptr(rstd), rows, n,
+                                           float(eps), _stream(x2d)))
+    return y, rstd
+
+
+def rmsnorm_bwd(g: torch.Tensor, x2d: torch.Tensor, w: torch.Tensor,
+                rstd: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """dx (bf16) and dw (bf16, fp32-accumulated) of rmsnorm."""
+    _on_gpu(g, x2d, w, rstd)
+    g = g.contiguous()
+    w = w.contiguous()
+    rows, n = x2d.shape
+    if g.shape != x2d.shape:
+        raise ValueError(f"grad shape {tuple(g.shape)} != {tuple(x2d.shape)}")
+    _bf16("grad", g)
+    dx = torch.empty_like(x2d)
+    dw = torch.empty(n, device=x2d.device, dtype=w.dtype)
+    nbytes = lib().krsi_rmsnorm_bwd_workspace_bytes(rows, n)
+    ws = torch.empty(max(nbytes, 1), device=x2d.device, dtype=torch.uint8)
+    _check(lib().krsi_rmsnorm_bwd_bf16(_ptr(g), _ptr(x2d), _ptr(w), _ptr(rstd), _ptr(dx), _ptr(dw),
+                                       _ptr(ws), nbytes, rows, n, _stream(x2d)))
+    return dx, dw
+
+
+# --------------------------------------------------------------------- GEGLU
+_APPROX = {"tanh": 1, "none": 0}
+
+
+def _approx(approximate: str) -> int:
+    if approximate not in _APPROX:
+        raise ValueError(f"approximate must be 'tanh' or 'none', got {approximate!r}")
+    return _APPROX[approximate]
+
+
+def geglu_fwd(u: torch.Tensor, approximate: str = "tanh") -> torch.Tensor:
+    _on_gpu(u)
+    _bf16("u", u)
+    if u.dim() != 2 or not u.is_contiguous() or u.shape[1] % 2:
+        raise ValueError("u must be a contiguous [rows, 2F] tensor")
+    rows, f2 = u.shape
+    out = torch.empty(rows, f2 // 2, device=u.device, dtype=u.dtype)
+    if rows and f2:
+        _check(lib().krsi_geglu_fwd_bf16(_ptr(u), _ptr(out), rows, f2 // 2, _approx(approximate),
+                                         _stream(u)))
+    return out
+
+
+def geglu_bwd(g: torch.Tensor, u: torch.Tensor, approximate: str = "tanh") -> torch.Tensor:
+    _on_gpu(g, u)
+    g = g.contiguous()
+    _bf16("grad", g)
+    rows, f2 = u.shape
+    if g.shape != (rows, f2 // 2):
+        raise ValueError(f"grad shape {tuple(g.shape)} != {(rows, f2 // 2)}")
+    du = torch.empty_like(u)
+    if rows and f2:
+        _check(lib().krsi_geglu_bwd_bf16(_ptr(g), _ptr(u), _ptr(du), rows, f2 // 2,
+                                         _approx(approximate), _stream(u)))
+    return du
+
+
+# ------------------------------------------------ relative-position attention
+def _check_relpos(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: int) -> None:
+    _on_gpu(qkv, pd)
+    _bf16("qkv", qkv)
+    if pd.dtype != torch.float32:
+        raise TypeError(f"pd must be torch.float32, got {pd.dtype}")
+    if qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a 2D [B*S, >=3*H*D] tensor with unit column stride")
+    if qkv.shape[0] != B * S or qkv.shape[1] < 3 * H * D:
+        raise ValueError(f"qkv shape {tuple(qkv.shape)} does not hold B*S={B * S} rows of 3*H*D={3 * H * D}")
+    if tuple(pd.shape) != (H, 2 * S - 1):
+        raise ValueError(f"pd shape {tuple(pd.shape)} != {(H, 2 * S - 1)}")
+    if D % 8 or not 8 <= D <= 128:
+        raise ValueError(f"head dim D={D} unsupported: needs D % 8 == 0 and 8 <= D <= 128")
+
+
+def relpos_fwd(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: int,
+               scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """out (bf16), out32 (fp32) [B*S, H*D] and lse [B*H, S] (log2 domain)."""
+    _check_relpos(qkv, pd, B, S, H, D)
+    pd = pd.contiguous()
+    out = torch.empty(B * S, H * D, device=qkv.device, dtype=qkv.dtype)
+    out32 = torch.empty(B * S, H * D, device=qkv.device, dtype=torch.float32)
+    lse = torch.empty(B * H, S, device=qkv.device, dtype=torch.float32)
+    _check(lib().krsi_relpos_fwd_bf16(_ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out), _ptr(out32),
+                                      _ptr(lse), B, S, H, D, float(scale), _stream(qkv)))
+    return out, out32, lse
+
+
+def relpos_bwd(dout: torch.Tensor, qkv: torch.Tensor, pd: torch.Tensor, out32: torch.Tensor,
+               lse: torch.Tensor, B: int, S: int, H: int, D: int,
+               scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """dqkv (same shape and strides as a contiguous qkv) and dpd [H, 2S-1] fp32."""
+    _check_relpos(qkv, pd, B, S, H, D)
+    _on_gpu(dout, out32, lse)
+    dout = dout.contiguous()
+    _bf16("grad", dout)
+    pd = pd.contiguous()
+    # Every column of dqkv is written (q, k and v slots of each head); columns
+    # past 3*H*D of a wider qkv are zero, as the gradient of a slice.
+    dqkv = torch.empty(qkv.shape, device=qkv.device, dtype=qkv.dtype)
+    if qkv.shape[1] > 3 * H * D:
+        dqkv[:, 3 * H * D:].zero_()
+    dpd = torch.empty(H, 2 * S - 1, device=qkv.device, dtype=torch.float32)
+    nbytes = lib().krsi_relpos_bwd_workspace_bytes(B, S, H, D)
+    ws = torch.empty(nbytes, device=qkv.device, dtype=torch.uint8)
+    _check(lib().krsi_relpos_bwd_bf16(_ptr(dout), _ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out32),
+                                      _ptr(lse), _ptr(dqkv), dqkv.stride(0), _ptr(dpd), _ptr(ws), nbytes,
+                                      B, S, H, D, float(scale), _stream(qkv)))
+    return dqkv, dpd

@@ -1,0 +1,59 @@
+"""GEGLU forward + backward on a merged [a | b] GEMM output, on hand-written gfx950 (MI355X)
+HIP kernels. Use geglu(u) (differentiable, torch.compile-friendly).
+
+u: [rows, 2F] (the output of x @ cat([W_gate, W_up]).T); returns gelu_tanh(u[:, :F]) * u[:, F:], with
+the same bf16 rounding points as eager. Backward writes d[a | b] in one pass, so the merged GEMM's
+backward reads one gradient tensor. geglu(u, approximate="none") selects the exact (erf) GELU.
+Drop-in for the reference's library/geglu.py (same functions and arguments; geglu.py:104-120).
+"""
+import sys
+from pathlib import Path
+
+import torch
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+import _hip  # noqa: E402
+from _compat import compiling  # noqa: E402
+
+
+def _ops():
+    import _ops as ops  # noqa: PLC0415 - registers the krsi:: ops on first use
+    return ops
+
+
+class GEGLU(torch.autograd.Function):
+    """Eager path: launches the kernels directly (reference: geglu.py:71-82)."""
+
+    @staticmethod
+    def forward(ctx, u, approximate):
+        ctx.save_for_backward(u)
+        ctx.approximate = approximate
+        return _hip.geglu_fwd(u, approximate)
+
+    @staticmethod
+    def backward(ctx, g):
+        (u,) = ctx.saved_tensors
+        return _hip.geglu_bwd(g.contiguous(), u, ctx.approximate), None
+
+
+def geglu(u, *, approximate="tanh"):
+    """gelu(u[:, :F]) * u[:, F:] for a contiguous [rows, 2F] tensor (tanh GELU by default)."""
+    if compiling():
+        return _ops().geglu_fwd_op(u, approximate)
+    return GEGLU.apply(u, approximate)
+
+
+def reference(u, *, approximate="tanh"):
+    a, b = u.chunk(2, dim=-1)
+    return torch.nn.functional.gelu(a, approximate=approximate) * b
+
+
+def selftest():
+    from _harness import selftest_autograd  # noqa: PLC0415
+
+    u = torch.randn(2048, 2 * 2816, device="cuda", dtype=torch.bfloat16)
+    return selftest_autograd(geglu, reference, [u])
+
+
+if __name__ == "__main__":
+    print(selftest())

@@ -1,0 +1,75 @@
+"""Flash attention forward + backward with an additive bias that depends only on (j - i), on
+hand-written gfx950 (MI355X) HIP kernels (bf16 MFMA, fp32 softmax).
+
+relpos_attention(qkv, pd, B, S, H, D, scale) -> [B*S, H*D]   (differentiable, torch.compile-friendly)
+  qkv: [B*S, 3*H*D] (the fused q|k|v GEMM output, read in place: no permute copies; any row stride)
+  pd:  [H, 2S-1] fp32 per-distance bias, bias[h, i, j] = pd[h, j - i + S - 1] (T5 relative position,
+       ALiBi, any Toeplitz bias); its gradient is reduced along the diagonals of dS inside the
+       backward kernels (no [B, H, S, S] buffer, no scatter).
+Backward keeps an fp32 copy of O for delta = rowsum(dO * O). No causal mask; D % 8 == 0, D <= 128
+(so D = 72 runs too). Drop-in for the reference's library/relpos_attention.py (same functions and
+arguments; relpos_attention.py:198-222).
+"""
+import sys
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+
+sys.path.insert(0, str(Path(__file__).resolve().parent))
+import _hip  # noqa: E402
+from _compat import compiling  # noqa: E402
+
+LOG2E = 1.4426950408889634
+
+
+def _ops():
+    import _ops as ops  # noqa: PLC0415 - registers the krsi:: ops on first use
+    return ops
+
+
+class RelPosAttention(torch.autograd.Function):
+    """Eager path: launches the kernels directly (reference: relpos_attention.py:160-172)."""
+
+    @staticmethod
+    def forward(ctx, qkv, pd, B, S, H, D, scale):
+        out, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, scale)
+        ctx.save_for_backward(qkv, pd, out32, lse)
+        ctx.dims = (B, S, H, D, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        dqkv, dpd = _hip.relpos_bwd(dout.contiguous(), *ctx.saved_tensors, *ctx.dims)
+        return dqkv, dpd, None, None, None, None, None
+
+
+def relpos_attention(qkv, pd, B, S, H, D, scale):
+    if compiling():
+        return _ops().relpos_fwd_op(qkv, pd, B, S, H, D, scale)[0]
+    return RelPosAttention.apply(qkv, pd, B, S, H, D, scale)
+
+
+def reference(qkv, pd, B, S, H, D, scale):
+    q, k, v = qkv.view(B, S, 3, H, D).permute(2, 0, 3, 1, 4)
+    pos = torch.arange(S, device=qkv.device)
+    bias = pd[:, pos[None, :] - pos[:, None] + S - 1][None].to(qkv.dtype)
+    from torch.nn.attention import SDPBackend, sdpa_kernel  # noqa: PLC0415
+
+    with sdpa_kernel(SDPBackend.MATH):
+        o = F.scaled_dot_product_attention(q, k, v, attn_mask=bias, scale=scale)
+    return o.transpose(1, 2).reshape(B * S, H * D)
+
+
+def selftest():
+    from _harness import selftest_autograd  # noqa: PLC0415
+
+    B, S, H, D = 4, 512, 16, 64
+    qkv = (0.6 * torch.randn(B * S, 3 * H * D, device="cuda")).to(torch.bfloat16)
+    pd = torch.randn(H, 2 * S - 1, device="cuda")
+    return selftest_autograd(lambda q, p: relpos_attention(q, p, B, S, H, D, 1.0),
+                             lambda q, p: reference(q, p, B, S, H, D, 1.0), [qkv, pd])
+
+
+if __name__ == "__main__":
+    print(selftest())

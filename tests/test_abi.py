@@ -1,0 +1,141 @@
+"""The C-ABI boundary without a GPU: the library loads, exports every entry point of
+include/krsi.h with the declared signature, binds to torch's HIP runtime, reports errors
+for invalid arguments before launching anything, and the Python layer has no CPU path."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "krsi.h"
+NULL = None
+FAKE = 0x10000  # a 16-byte aligned non-null address; never dereferenced on these paths
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(krsi_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_python_binding_set():
+    assert declared() == sorted(_hip.SIGNATURES)
+
+
+def test_library_loads_and_exports_every_symbol():
+    lib = _hip.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.krsi_abi_version() == _hip.ABI_VERSION
+
+
+def test_single_hip_runtime_in_process():
+    _hip.lib()
+    maps = Path("/proc/self/maps").read_text()
+    paths = {m for m in re.findall(r"\S*libamdhip64\.so\S*", maps)}
+    assert len(paths) <= 1, paths
+
+
+def test_error_strings():
+    lib = _hip.lib()
+    for code in range(0, 8):
+        s = lib.krsi_error_string(code).decode()
+        assert s and ("krsi" in s or code == 0)
+    assert "unknown" in lib.krsi_error_string(99).decode()
+
+
+def test_workspace_sizes():
+    lib = _hip.lib()
+    a = lib.krsi_rmsnorm_bwd_workspace_bytes(32768, 4096)
+    assert a > 0 and a % 256 == 0
+    assert lib.krsi_rmsnorm_bwd_workspace_bytes(0, 4096) == 0
+    assert lib.krsi_rmsnorm_bwd_workspace_bytes(10, 0) == 0
+    b = lib.krsi_relpos_bwd_workspace_bytes(4, 4096, 16, 64)
+    # delta [B,H,S] + one fp32 partial row of S+128 diagonals per 128-query block
+    assert b >= 4 * 16 * 4096 * 4 + 4 * 16 * 32 * (4096 + 128) * 4
+    assert lib.krsi_relpos_bwd_workspace_bytes(0, 4096, 16, 64) == 0
+
+
+def test_validation_before_launch():
+    lib = _hip.lib()
+    E = {"NULL": 1, "SHAPE": 2, "ALIGN": 3, "WS": 4, "UNSUP": 5, "SCALE": 7}
+    # RMSNorm
+    assert lib.krsi_rmsnorm_fwd_bf16(FAKE, FAKE, FAKE, FAKE, 4, 0, 1e-6, NULL) == E["SHAPE"]
+    assert lib.krsi_rmsnorm_fwd_bf16(FAKE, FAKE, FAKE, FAKE, 4, 16385, 1e-6, NULL) == E["SHAPE"]
+    assert lib.krsi_rmsnorm_fwd_bf16(NULL, FAKE, FAKE, FAKE, 4, 64, 1e-6, NULL) == E["NULL"]
+    assert lib.krsi_rmsnorm_fwd_bf16(FAKE, FAKE, FAKE, FAKE, 4, 64, float("nan"), NULL) == E["SCALE"]
+    assert lib.krsi_rmsnorm_fwd_bf16(NULL, NULL, NULL, NULL, 0, 64, 1e-6, NULL) == 0   # empty: no-op
+    assert lib.krsi_rmsnorm_bwd_bf16(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 64, 64, NULL) == E["WS"]
+    assert lib.krsi_rmsnorm_bwd_bf16(FAKE, FAKE, FAKE, FAKE, FAKE, NULL, FAKE, 1 << 30, 64, 64, NULL) == E["NULL"]
+    # GEGLU
+    assert lib.krsi_geglu_fwd_bf16(FAKE, FAKE, 4, 0, 1, NULL) == E["SHAPE"]
+    assert lib.krsi_geglu_fwd_bf16(FAKE, FAKE, 4, 8, 2, NULL) == E["UNSUP"]
+    assert lib.krsi_geglu_bwd_bf16(FAKE, NULL, FAKE, 4, 8, 0, NULL) == E["NULL"]
+    # Attention
+    args = dict(B=2, S=16, H=2, D=64)
+
+    def fwd(qkv=FAKE, ld=384, pd=FAKE, out=FAKE, B=2, S=16, H=2, D=64, scale=0.125):
+        return lib.krsi_relpos_fwd_bf16(qkv, ld, pd, out, FAKE, FAKE, B, S, H, D, scale, NULL)
+
+    assert fwd(D=12, ld=72) == E["UNSUP"]
+    assert fwd(D=136, ld=816) == E["UNSUP"]
+    assert fwd(S=0) == E["SHAPE"]
+    assert fwd(ld=380) == E["SHAPE"]
+    assert fwd(ld=388) == E["ALIGN"]
+    assert fwd(qkv=FAKE + 2) == E["ALIGN"]
+    assert fwd(scale=float("inf")) == E["SCALE"]
+    assert fwd(pd=NULL) == E["NULL"]
+    assert fwd(B=40000, H=2) == E["SHAPE"]   # B*H above the grid limit
+    ws = lib.krsi_relpos_bwd_workspace_bytes(args["B"], args["S"], args["H"], args["D"])
+    assert lib.krsi_relpos_bwd_bf16(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 384, FAKE, FAKE, ws - 1,
+                                    2, 16, 2, 64, 0.125, NULL) == E["WS"]
+    assert lib.krsi_relpos_bwd_bf16(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 200, FAKE, FAKE, ws,
+                                    2, 16, 2, 64, 0.125, NULL) == E["SHAPE"]
+
+
+def test_python_layer_has_no_cpu_path():
+    import geglu
+    import relpos_attention
+    import rmsnorm
+
+    x = torch.randn(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        rmsnorm.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="GPU"):
+        geglu.geglu(x)
+    qkv = torch.randn(8, 3 * 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        relpos_attention.relpos_attention(qkv, torch.zeros(1, 15), 1, 8, 1, 64, 0.125)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_hip, "LIB_PATH", tmp_path / "libkrsi_hip.so")
+    monkeypatch.setattr(_hip, "_lib", None)
+    with pytest.raises(ImportError, match="not built"):
+        _hip.lib()
+
+
+def test_product_never_imports_the_oracle():
+    for p in (ROOT / "kernel-rsi_amd").rglob("*.py"):
+        if p.name == "build.py":
+            continue
+        assert "oracle" not in p.read_text(), p
+
+
+def test_modules_keep_the_reference_interface():
+    import inspect
+
+    import geglu
+    import relpos_attention
+    import rmsnorm
+
+    assert list(inspect.signature(rmsnorm.rmsnorm).parameters) == ["x2d", "w", "eps"]
+    assert list(inspect.signature(rmsnorm.reference).parameters) == ["x2d", "w", "eps"]
+    assert list(inspect.signature(geglu.geglu).parameters)[0] == "u"
+    assert list(inspect.signature(relpos_attention.relpos_attention).parameters) == \
+        ["qkv", "pd", "B", "S", "H", "D", "scale"]
+    for m in (rmsnorm, geglu, relpos_attention):
+        assert callable(m.selftest) and callable(m.reference)

@@ -1,0 +1,101 @@
+"""RMSNorm HIP kernels vs the fp32 reference on the GPU (parity tests proper)."""
+import pytest
+import torch
+
+import krsi_oracle as O
+import rmsnorm as R
+from krsi_testutil import assert_parity, log, seeded
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-6
+
+
+def _run(x, w, g, eps=EPS):
+    """ref32 (fp32 autograd of the reference formula), eager bf16 original, HIP kernel."""
+    ref32 = O.rmsnorm_train(x, w, eps, g.float(), torch.float32)
+    orig = O.rmsnorm_train(x, w, eps, g, torch.bfloat16)
+    xx = x.detach().requires_grad_(True)
+    ww = w.detach().requires_grad_(True)
+    y = R.rmsnorm(xx, ww, eps)
+    dx, dw = torch.autograd.grad(y, [xx, ww], g)
+    return ref32, orig, (y.detach(), dx, dw)
+
+
+@pytest.mark.parametrize("rows", [2048, 300])
+def test_rmsnorm_fwd_cpu_config(rows):
+    """x [2,1024,1152] (and ragged [1,300,1152]) ~N(0,1), w ~N(1,0.02)."""
+    log(f"rmsnorm fwd rows={rows} n=1152")
+    x = seeded((rows, 1152), 0)
+    w = seeded((1152,), 1, std=0.02, mean=1.0)
+    g = seeded((rows, 1152), 2)
+    ref32, orig, cand = _run(x, w, g)
+    assert_parity(["y", "dx", "dw"], ref32, orig, cand)
+    # rstd against fp32, and y bitwise against eager bf16 except at rounding ties of x*r.
+    import _hip
+
+    y, rstd = _hip.rmsnorm_fwd(x, w, EPS)
+    r32 = torch.rsqrt(x.float().pow(2).mean(-1) + EPS)
+    assert torch.allclose(rstd, r32, rtol=2e-6, atol=0)
+    same = (y == O.rmsnorm(x, w, EPS)).float().mean().item()
+    assert same > 0.999, same
+
+
+def test_rmsnorm_train_step_full():
+    """x [8,4096,4096] fwd+bwd, y, dx and dw vs fp32 autograd."""
+    log("rmsnorm fwd+bwd rows=32768 n=4096")
+    x = seeded((32768, 4096), 0)
+    w = seeded((4096,), 1, std=0.02, mean=1.0)
+    g = seeded((32768, 4096), 2)
+    ref32, orig, cand = _run(x, w, g)
+    assert_parity(["y", "dx", "dw"], ref32, orig, cand)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 8), (3, 1), (5, 7), (64, 1000), (33, 1001), (17, 2048),
+                                    (40, 4104), (9, 8192), (7, 12288), (5, 16384), (1000, 512)])
+def test_rmsnorm_shapes(rows, n):
+    log(f"rmsnorm shapes rows={rows} n={n}")
+    x = seeded((rows, n), 10 + n)
+    w = seeded((n,), 11, std=0.1, mean=1.0)
+    g = seeded((rows, n), 12)
+    ref32, orig, cand = _run(x, w, g)
+    assert_parity(["y", "dx", "dw"], ref32, orig, cand)
+
+
+def test_rmsnorm_unaligned_view_takes_scalar_path():
+    log("rmsnorm unaligned view")
+    base = seeded((64 * 256 + 1,), 3)
+    x = base[1:].view(64, 256)            # 2-byte offset: not 16-byte aligned
+    w = seeded((256,), 4, std=0.1, mean=1.0)
+    g = seeded((64, 256), 5)
+    ref32, orig, cand = _run(x, w, g)
+    assert_parity(["y", "dx", "dw"], ref32, orig, cand)
+
+
+def test_rmsnorm_empty_rows():
+    x = torch.empty(0, 64, device="cuda", dtype=torch.bfloat16)
+    w = seeded((64,), 1)
+    xx, ww = x.requires_grad_(True), w.detach().requires_grad_(True)
+    y = R.rmsnorm(xx, ww, EPS)
+    assert y.shape == (0, 64)
+    dx, dw = torch.autograd.grad(y, [xx, ww], torch.empty_like(y))
+    assert dx.shape == (0, 64) and torch.count_nonzero(dw) == 0
+
+
+def test_rmsnorm_backward_deterministic():
+    log("rmsnorm determinism")
+    import _hip
+
+    x = seeded((4096, 4096), 0)
+    w = seeded((4096,), 1, std=0.02, mean=1.0)
+    g = seeded((4096, 4096), 2)
+    _, rstd = _hip.rmsnorm_fwd(x, w, EPS)
+    a = _hip.rmsnorm_bwd(g, x, w, rstd)
+    b = _hip.rmsnorm_bwd(g, x, w, rstd)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_rmsnorm_rejects_cpu_and_wrong_dtype():
+    with pytest.raises(ValueError):
+        R.rmsnorm(torch.randn(4, 8, dtype=torch.bfloat16), torch.ones(8, dtype=torch.bfloat16), EPS)
+    with pytest.raises(TypeError):
+        R.rmsnorm(torch.randn(4, 8, device="cuda"), torch.ones(8, device="cuda"), EPS)
