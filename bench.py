@@ -223,6 +223,25 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False) -> dict:
     return res
 
 
+def measured_copy_gbs() -> float:
+    """Achievable HBM rate on this box: a 2 GiB device-to-device copy (read + write bytes)."""
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    del a, b
+    return round(2 * 2 * n / (ms * 1e-3) / 1e9, 1)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +277,7 @@ def main() -> None:
         "roofline": head["roofline"],
         "cpu_baseline": {**head.get("cpu_baseline", {}), "cpu": _cpu_model()} if "cpu_baseline" in head else None,
         "components": comps,
+        "measured_peaks": {"hbm_copy_GB/s": measured_copy_gbs()},
     }
     print(json.dumps(line))
 

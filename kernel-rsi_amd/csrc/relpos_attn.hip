@@ -12,34 +12,38 @@
 //              dpd[h, k] = sum over b, i, j with j - i + S - 1 = k of ds     (:154-156)
 //
 // Layout and tiling (MI355X-native, not the reference's):
-//   * Wave64 owns 32 queries (forward, dQ) or 32 keys (dK/dV); a workgroup of
-//     4 waves owns 128. The register-resident side (Q and dO, or K and V) is
-//     loaded once as MFMA B operands straight from HBM with 128-bit loads.
-//   * The streamed side is staged per iteration in LDS, row-major for the
-//     products that contract over the head dim and transposed (head dim x
-//     position, 8-row XOR swizzle) for the products that contract over
-//     positions. Global loads of iteration t+1 are issued before the MFMAs of
-//     iteration t (register double buffering).
+//   * A wavefront owns 32 queries (forward, dQ) or 32 keys (dK/dV); a
+//     workgroup of NW wavefronts owns 32*NW. The register-resident side (Q and
+//     dO, or K and V) is loaded once from HBM with 128-bit loads straight into
+//     MFMA operand registers.
+//   * The streamed side (64 positions per step) is staged in LDS row-major
+//     with 128-bit writes only. Products that contract over the head dim read
+//     it with 128-bit row reads; products that contract over positions read it
+//     with ds_read_b64_tr_b16, which returns, per lane, 4 consecutive rows of
+//     one column of a 4x16 block, so no transposed copy is ever written.
+//     Global loads of step t+1 are issued before the MFMAs of step t.
 //   * Scores are computed transposed (S^T = K Q^T) in the forward and dQ
-//     kernels, so each lane owns one query: row max and row sum are in-lane
+//     kernels, so each lane owns one query: the row max and row sum are in-lane
 //     reductions plus one cross-half exchange, and lse/delta are registers.
-//     The fp32 score tile is converted in place to the B operand of the next
-//     MFMA; the K-dimension permutation this implies is mirrored in the LDS
-//     layout of the other operand (perm_pos).
-//   * The Toeplitz bias is staged once per iteration as a window of
-//     BM + BN - 1 entries (times log2 e), in 4 copies shifted by one element,
-//     so every lane fetches its 4 consecutive entries with one aligned 128-bit
-//     LDS read.
-//   * Online softmax keeps the exact running max per 64-key block (so the
-//     block maximum gives p = 1, exact in bf16, as in the reference); the
-//     fp32 accumulators are rescaled only when some lane's max moved.
+//     The fp32 score tile is converted in place to the bf16 operand of the next
+//     MFMA: registers 8u..8u+7 of half-wave g hold positions 16u + 4g + {0..3}
+//     and 16u + 8 + 4g + {0..3}, exactly the two 4-row groups two transposed
+//     reads return, so the K order of both operands agrees without shuffles.
+//   * The Toeplitz bias of a (32*NW) x 64 tile is a window of consecutive table
+//     entries, staged once per step (times log2 e) in 4 copies shifted by one
+//     entry, so every lane reads its 4 consecutive entries with one aligned
+//     128-bit LDS read.
+//   * Online softmax keeps the exact running max per 64-key step (the step
+//     maximum gives p = 1, exact in bf16, as in the reference); the fp32
+//     accumulators are rescaled only when some lane's max moved.
 //   * dpd is reduced along the diagonals j - i inside the dQ kernel: each
-//     (wave, half-wave) adds its fp32 ds into a private 256-entry LDS ring
-//     indexed by diagonal (collision-free, so a plain read-modify-write in
-//     program order is exact and deterministic), the
-//     finished diagonals are folded in a fixed order into one partial row per
-//     128-query block, and a last kernel sums the partial rows over batch and
-//     query blocks in a fixed order. No [B, H, S, S] buffer exists.
+//     (wave, half-wave) adds its fp32 ds into a private LDS ring indexed by
+//     diagonal. Within one register the 32 lanes of a half-wave hit distinct
+//     slots and a wave's LDS operations complete in order, so a plain
+//     read-modify-write is exact and deterministic. Diagonals that can get no
+//     further contribution are folded in a fixed order into one partial row per
+//     query block; a last kernel sums the partial rows over batch and query
+//     blocks in a fixed order. No [B, H, S, S] buffer exists.
 #include <math.h>
 
 #include "krsi_device.h"
@@ -48,13 +52,7 @@
 namespace krsi {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kRows = 128;     // queries (forward, dQ) or keys (dK/dV) per workgroup
-constexpr int kStep = 64;      // streamed positions per iteration
-constexpr int kTLD = kStep + 8;            // transposed tile row stride (bf16)
-constexpr int kWin = kRows + kStep - 1;    // bias window entries
-constexpr int kWLD = 196;                  // bias copy length (>= kWin + 3, multiple of 4)
-constexpr int kRing = 256;                 // dpd ring entries per (wave, half)
+constexpr int kStep = 64;  // streamed positions per iteration
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DP>
@@ -62,96 +60,114 @@ struct Geo {
   static constexpr int KS = DP / 16;         // K steps of 16 over the head dim
   static constexpr int DB = (DP + 31) / 32;  // 32-wide head-dim blocks of head-dim outputs
   static constexpr int DPV = DB * 32;
-  static constexpr int KLD = DP + 8;         // row-major tile stride (bf16)
-  static constexpr int CPR = DP / 8;         // 16-byte chunks per row
+  static constexpr int RLD = DPV + 8;        // row-major tile stride (bf16), padded
+  static constexpr int CPR = DP / 8;         // 16-byte chunks per staged row
   static constexpr int NCH = kStep * CPR;    // chunks per streamed tile
-  static constexpr int CPT = (NCH + kThreads - 1) / kThreads;
 };
 
-constexpr int kBPT = (4 * kWLD + kThreads - 1) / kThreads;  // bias entries per thread
+template <int NW>
+struct Blk {
+  static constexpr int ROWS = 32 * NW;             // queries or keys per workgroup
+  static constexpr int NT = 64 * NW;               // threads per workgroup
+  static constexpr int WLD = ROWS + kStep + 4;     // bias copy length (multiple of 4)
+  static constexpr int WIN = WLD - 3;              // distinct window entries loaded
+  static constexpr int BPT = (WIN + NT - 1) / NT;  // window entries per thread
+  static constexpr int RING = ROWS <= 128 ? 256 : 512;  // dpd ring (>= ROWS + 2 * kStep - 1)
+};
 
-// Position of streamed element `pos` (0..63) in a transposed tile row `d`.
-// Bits 2 and 3 are swapped so that the 8 positions a lane needs for one MFMA
-// step are contiguous (the K order of an fp32 D tile reused as a bf16
-// operand: registers 8u..8u+7 of half g hold positions 16u + 4g + {0..3} and
-// 16u + 8 + 4g + {0..3}); bits 3..5 are XORed with (d / 8) % 8 so that the
-// transposing 16-bit writes of 8 consecutive head-dim rows hit 8 banks.
-__device__ __forceinline__ int perm_pos(int d, int pos) {
-  const int p = (pos & ~12) | ((pos >> 1) & 4) | ((pos << 1) & 8);
-  return p ^ (((d >> 3) & 7) << 3);
-}
-
-// Start of the 8 contiguous positions holding MFMA step `base` (a multiple of
-// 8 before permutation) for head-dim row d.
-__device__ __forceinline__ int perm_base(int d, int base) { return base ^ (((d >> 3) & 7) << 3); }
-
-__device__ __forceinline__ uint16_t elem16(const u32x4& v, int e) {
-  return (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
-}
-
-__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr u32x4 kZero4 = {0u, 0u, 0u, 0u};
 
-// Stage one streamed tile of kStep rows x DP columns: row-major into `rm`
-// (may be null) and transposed into `tr` (may be null).
-template <int DP>
-__device__ __forceinline__ void stash_tile(const u32x4* regs, uint16_t* rm, uint16_t* tr) {
-  using G = Geo<DP>;
-#pragma unroll
-  for (int k = 0; k < G::CPT; ++k) {
-    const int c = threadIdx.x + k * kThreads;
-    if (c < G::NCH) {
-      const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
-      if (rm) *reinterpret_cast<u32x4*>(rm + row * G::KLD + d0) = regs[k];
-      if (tr) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tr[(d0 + e) * kTLD + perm_pos(d0 + e, row)] = elem16(regs[k], e);
-      }
-    }
-  }
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// MFMA operand whose 8 K values are rows [k0, k0+4) and [k1, k1+4) of column
+// c0 + (lane % 16) of a row-major LDS tile (stride ld): two transposed reads,
+// in each of which lane s of a 16-lane group supplies row (k + s/4), columns
+// c0 + 4 (s % 4) .. +3. The caller passes c0 = block + 16 * ((lane / 16) % 2),
+// so lane l receives column block + l % 32.
+__device__ __forceinline__ u32x4 tr_operand(const uint16_t* tile, int ld, int k0, int k1, int c0) {
+  const int s = threadIdx.x & 15;
+  const int off = (s >> 2) * ld + c0 + 4 * (s & 3);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + k0 * ld + off));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + k1 * ld + off));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return u32x4{ua.x, ua.y, ub.x, ub.y};
 }
 
 // Load one streamed tile (rows p0..p0+63 of a [*, ld] bf16 matrix whose
 // column block starts at `col`) into registers, zero outside [0, S) x [0, D).
-template <int DP>
+template <int DP, int NT>
 __device__ __forceinline__ void load_tile(u32x4* regs, const uint16_t* col, int64_t ld, int64_t tok0,
                                           int p0, int S, int D) {
   using G = Geo<DP>;
+  constexpr int CPT = (G::NCH + NT - 1) / NT;
 #pragma unroll
-  for (int k = 0; k < G::CPT; ++k) {
-    const int c = threadIdx.x + k * kThreads;
+  for (int k = 0; k < CPT; ++k) {
+    const int c = threadIdx.x + k * NT;
     const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
     const bool ok = c < G::NCH && p0 + row < S && d0 < D;
     regs[k] = ok ? ld16(col + (tok0 + p0 + row) * ld + d0) : kZero4;
   }
 }
 
-// Bias window: copy cc, position y holds T[wb + sgn * (y - cc)] * log2(e),
-// zero outside [0, 2S - 1).
+template <int DP, int NT>
+__device__ __forceinline__ void stash_tile(const u32x4* regs, uint16_t* tile) {
+  using G = Geo<DP>;
+  constexpr int CPT = (G::NCH + NT - 1) / NT;
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int c = threadIdx.x + k * NT;
+    if (c < G::NCH) {
+      const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
+      *reinterpret_cast<u32x4*>(tile + row * G::RLD + d0) = regs[k];
+    }
+  }
+}
+
+// Columns [DP, DPV) of a row-major tile are read by the transposed reads of the
+// last head-dim block and never staged: zero them once.
+template <int DP, int NT>
+__device__ __forceinline__ void zero_pad_cols(uint16_t* tile) {
+  using G = Geo<DP>;
+  constexpr int W = G::DPV - DP;
+  if (W > 0)
+    for (int e = threadIdx.x; e < kStep * W; e += NT) tile[(e / W) * G::RLD + DP + e % W] = 0;
+}
+
+// Bias window entry x (0 <= x < WIN) holds T[wb + sgn * x] * log2(e), zero
+// outside [0, 2S - 1); it is stored at position x + cc of copy cc.
+template <int NW>
 __device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn) {
+  using K = Blk<NW>;
 #pragma unroll
-  for (int k = 0; k < kBPT; ++k) {
-    const int e = threadIdx.x + k * kThreads;
-    const int cc = e / kWLD, y = e - cc * kWLD;
-    const int src = wb + sgn * (y - cc);
-    regs[k] = (e < 4 * kWLD && src >= 0 && src < npd) ? pdh[src] * kLog2e : 0.f;
+  for (int k = 0; k < K::BPT; ++k) {
+    const int x = threadIdx.x + k * K::NT;
+    const int src = wb + sgn * x;
+    regs[k] = (x < K::WIN && src >= 0 && src < npd) ? pdh[src] * kLog2e : 0.f;
   }
 }
 
+template <int NW>
 __device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
+  using K = Blk<NW>;
 #pragma unroll
-  for (int k = 0; k < kBPT; ++k) {
-    const int e = threadIdx.x + k * kThreads;
-    if (e < 4 * kWLD) bw[e] = regs[k];
+  for (int k = 0; k < K::BPT; ++k) {
+    const int x = threadIdx.x + k * K::NT;
+    if (x < K::WIN) {
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) bw[cc * K::WLD + x + cc] = regs[k];
+    }
   }
 }
 
-// The 16 bias values of one 32x32 D tile: entries x0 + 8a + b (a, b = 0..3)
-// of the window, read from the copy that makes x0 16-byte aligned.
+// The 16 bias values of one 32x32 D tile: window entries x0 + 8a + b
+// (a, b = 0..3), read from the copy that makes x0 16-byte aligned.
+template <int NW>
 __device__ __forceinline__ void read_bias16(const float* bw, int x0, float* out) {
   const int cc = (-x0) & 3;
-  const float* p = bw + cc * kWLD + x0 + cc;
+  const float* p = bw + cc * Blk<NW>::WLD + x0 + cc;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const f32x4 v = *reinterpret_cast<const f32x4*>(p + 8 * a);
@@ -161,19 +177,21 @@ __device__ __forceinline__ void read_bias16(const float* bw, int x0, float* out)
 }
 
 // ------------------------------------------------------------------- forward
-template <int DP>
-__global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
+template <int DP, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
     int D, float c) {
   using G = Geo<DP>;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[G::DPV * kTLD];
-  __shared__ __attribute__((aligned(16))) float Bw[4 * kWLD];
+  using K = Blk<NW>;
+  constexpr int CPT = (G::NCH + K::NT - 1) / K::NT;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
+  __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int i_wg = blockIdx.x * kRows;
+  const int i_wg = blockIdx.x * K::ROWS;
   const int ii = wave * 32 + l32;
   const int qi = i_wg + ii;
   const bool qvalid = qi < S;
@@ -184,8 +202,9 @@ __global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
   const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
+  const int c0 = 16 * ((lane >> 4) & 1);
 
-  for (int e = tid; e < (G::DPV - DP) * kTLD; e += kThreads) Vt[DP * kTLD + e] = 0;
+  zero_pad_cols<DP, K::NT>(Vs);
 
   u32x4 qreg[G::KS];
 #pragma unroll
@@ -201,24 +220,24 @@ __global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  u32x4 kst[G::CPT], vst[G::CPT];
-  float bst[kBPT];
+  u32x4 kst[CPT], vst[CPT];
+  float bst[K::BPT];
   const int T = (S + kStep - 1) / kStep;
-  load_tile<DP>(kst, kcol, ld, tok0, 0, S, D);
-  load_tile<DP>(vst, vcol, ld, tok0, 0, S, D);
-  load_bias(bst, pdh, npd, 0 - i_wg - (kRows - 1) + S - 1, 1);
+  load_tile<DP, K::NT>(kst, kcol, ld, tok0, 0, S, D);
+  load_tile<DP, K::NT>(vst, vcol, ld, tok0, 0, S, D);
+  load_bias<NW>(bst, pdh, npd, 0 - i_wg - (K::ROWS - 1) + S - 1, 1);
 
   for (int t = 0; t < T; ++t) {
     const int j0 = t * kStep;
     __syncthreads();
-    stash_tile<DP>(kst, Ks, nullptr);
-    stash_tile<DP>(vst, nullptr, Vt);
-    stash_bias(bst, Bw);
+    stash_tile<DP, K::NT>(kst, Ks);
+    stash_tile<DP, K::NT>(vst, Vs);
+    stash_bias<NW>(bst, Bw);
     __syncthreads();
     if (t + 1 < T) {
-      load_tile<DP>(kst, kcol, ld, tok0, j0 + kStep, S, D);
-      load_tile<DP>(vst, vcol, ld, tok0, j0 + kStep, S, D);
-      load_bias(bst, pdh, npd, j0 + kStep - i_wg - (kRows - 1) + S - 1, 1);
+      load_tile<DP, K::NT>(kst, kcol, ld, tok0, j0 + kStep, S, D);
+      load_tile<DP, K::NT>(vst, vcol, ld, tok0, j0 + kStep, S, D);
+      load_bias<NW>(bst, pdh, npd, j0 + kStep - i_wg - (K::ROWS - 1) + S - 1, 1);
     }
 
     float sc[2][16];
@@ -229,9 +248,9 @@ __global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < G::KS; ++s)
-        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::KLD + 16 * s + 8 * g), qreg[s], acc);
+        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
       float bias[16];
-      read_bias16(Bw, kb * 32 + 4 * g + (kRows - 1) - ii, bias);
+      read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii, bias);
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[kb][r] = acc[r] * c + bias[r];
     }
@@ -248,7 +267,7 @@ __global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Exact running max, as the reference (relpos_attention.py:48-50): the block's largest
+    // Exact running max, as the reference (relpos_attention.py:48-50): the step's largest
     // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
     // some lane's max moved.
     const bool need = mx > m_run;
@@ -275,12 +294,10 @@ __global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const u32x4 pb = pack8(&sc[kb][8 * u]);
+        const int k0 = kb * 32 + 16 * u + 4 * g;
 #pragma unroll
-        for (int db = 0; db < G::DB; ++db) {
-          const int d = db * 32 + l32;
-          oacc[db] = mfma32x32x16(ld16(Vt + d * kTLD + perm_base(d, kb * 32 + 16 * u + 8 * g)), pb,
-                                  oacc[db]);
-        }
+        for (int db = 0; db < G::DB; ++db)
+          oacc[db] = mfma32x32x16(tr_operand(Vs, G::RLD, k0, k0 + 8, db * 32 + c0), pb, oacc[db]);
       }
   }
 
@@ -308,22 +325,24 @@ __global__ __launch_bounds__(kThreads, 2) void relpos_fwd_kernel(
 }
 
 // ------------------------------------------------ backward: delta, dQ and dpd
-template <int DP>
-__global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
+template <int DP, int NW>
+__global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ out32,
     const float* __restrict__ lse, float* __restrict__ delta_ws, float* __restrict__ part,
     uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H, int D, float c, float scale) {
   using G = Geo<DP>;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Kt[G::DPV * kTLD];
-  __shared__ __attribute__((aligned(16))) float Bw[4 * kWLD];
-  __shared__ float ring[8][kRing];
+  using K = Blk<NW>;
+  constexpr int CPT = (G::NCH + K::NT - 1) / K::NT;
+  constexpr int RING = K::RING;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
+  __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
+  __shared__ float ring[2 * NW][RING];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int i_wg = blockIdx.x * kRows;
+  const int i_wg = blockIdx.x * K::ROWS;
   const int ii = wave * 32 + l32;
   const int qi = i_wg + ii;
   const bool qvalid = qi < S;
@@ -334,12 +353,13 @@ __global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ke
   const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
-  const int RS = S + 128;  // partial row stride
-  const int rlen = S + kRows - 1;
+  const int RS = S + K::ROWS;         // partial row stride
+  const int rlen = S + K::ROWS - 1;   // diagonals one query block touches
   float* prow = part + ((int64_t)bh * gridDim.x + blockIdx.x) * RS;
+  const int c0 = 16 * ((lane >> 4) & 1);
 
-  for (int e = tid; e < (G::DPV - DP) * kTLD; e += kThreads) Kt[DP * kTLD + e] = 0;
-  for (int e = tid; e < 8 * kRing; e += kThreads) (&ring[0][0])[e] = 0.f;
+  zero_pad_cols<DP, K::NT>(Ks);
+  for (int e = tid; e < 2 * NW * RING; e += K::NT) (&ring[0][0])[e] = 0.f;
 
   // Register-resident operands and per-query statistics.
   u32x4 qreg[G::KS], doreg[G::KS];
@@ -373,33 +393,33 @@ __global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ke
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
 
   float* myring = ring[wave * 2 + g];
-  u32x4 kst[G::CPT], vst[G::CPT];
-  float bst[kBPT];
+  u32x4 kst[CPT], vst[CPT];
+  float bst[K::BPT];
   const int T = (S + kStep - 1) / kStep;
-  load_tile<DP>(kst, kcol, ld, tok0, 0, S, D);
-  load_tile<DP>(vst, vcol, ld, tok0, 0, S, D);
-  load_bias(bst, pdh, npd, 0 - i_wg - (kRows - 1) + S - 1, 1);
+  load_tile<DP, K::NT>(kst, kcol, ld, tok0, 0, S, D);
+  load_tile<DP, K::NT>(vst, vcol, ld, tok0, 0, S, D);
+  load_bias<NW>(bst, pdh, npd, 0 - i_wg - (K::ROWS - 1) + S - 1, 1);
 
   for (int t = 0; t < T; ++t) {
     const int j0 = t * kStep;
     __syncthreads();
-    stash_tile<DP>(kst, Ks, Kt);
-    stash_tile<DP>(vst, Vs, nullptr);
-    stash_bias(bst, Bw);
+    stash_tile<DP, K::NT>(kst, Ks);
+    stash_tile<DP, K::NT>(vst, Vs);
+    stash_bias<NW>(bst, Bw);
     __syncthreads();
     if (t + 1 < T) {
-      load_tile<DP>(kst, kcol, ld, tok0, j0 + kStep, S, D);
-      load_tile<DP>(vst, vcol, ld, tok0, j0 + kStep, S, D);
-      load_bias(bst, pdh, npd, j0 + kStep - i_wg - (kRows - 1) + S - 1, 1);
+      load_tile<DP, K::NT>(kst, kcol, ld, tok0, j0 + kStep, S, D);
+      load_tile<DP, K::NT>(vst, vcol, ld, tok0, j0 + kStep, S, D);
+      load_bias<NW>(bst, pdh, npd, j0 + kStep - i_wg - (K::ROWS - 1) + S - 1, 1);
     }
     // Diagonals r in [64(t-1), 64t) received their last contribution in
-    // iteration t-1: fold the 8 rings in order into the partial row.
+    // iteration t-1: fold the rings in order into the partial row.
     if (t > 0 && wave == 0) {
       const int r = (t - 1) * kStep + lane;
-      const int slot = r & (kRing - 1);
+      const int slot = r & (RING - 1);
       float v = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < 2 * NW; ++k) {
         v += ring[k][slot];
         ring[k][slot] = 0.f;
       }
@@ -413,12 +433,12 @@ __global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ke
       for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < G::KS; ++s) {
-        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::KLD + 16 * s + 8 * g), qreg[s], acc);
-        accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::KLD + 16 * s + 8 * g), doreg[s], accp);
+        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
+        accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), doreg[s], accp);
       }
       float bias[16];
-      const int x0 = kb * 32 + 4 * g + (kRows - 1) - ii;
-      read_bias16(Bw, x0, bias);
+      const int x0 = kb * 32 + 4 * g + (K::ROWS - 1) - ii;
+      read_bias16<NW>(Bw, x0, bias);
       const bool tail = j0 + kStep > S;
       float ds[16];
 #pragma unroll
@@ -428,31 +448,29 @@ __global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ke
         if (tail && j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
         ds[r] = p * (accp[r] - delta);
       }
-      // Diagonal of D-register r: j - i + 127 - i_wg = 64t + x0 + 8a + b. Within one
+      // Diagonal of D-register r: j - i + ROWS - 1 - i_wg = 64t + x0 + 8a + b. Within one
       // register the 32 lanes of a half hit 32 distinct slots of their own ring, and LDS
       // operations of a wave complete in order, so a plain read-modify-write is exact
       // (LDS float atomics cost ~30x more here).
 #pragma unroll
-      for (int r = 0; r < 16; ++r) myring[(j0 + x0 + 8 * (r >> 2) + (r & 3)) & (kRing - 1)] += ds[r];
+      for (int r = 0; r < 16; ++r) myring[(j0 + x0 + 8 * (r >> 2) + (r & 3)) & (RING - 1)] += ds[r];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const u32x4 dsb = pack8(&ds[8 * u]);
+        const int k0 = kb * 32 + 16 * u + 4 * g;
 #pragma unroll
-        for (int db = 0; db < G::DB; ++db) {
-          const int d = db * 32 + l32;
-          dq[db] = mfma32x32x16(ld16(Kt + d * kTLD + perm_base(d, kb * 32 + 16 * u + 8 * g)), dsb,
-                                dq[db]);
-        }
+        for (int db = 0; db < G::DB; ++db)
+          dq[db] = mfma32x32x16(tr_operand(Ks, G::RLD, k0, k0 + 8, db * 32 + c0), dsb, dq[db]);
       }
     }
   }
 
   __syncthreads();
-  for (int r = (T - 1) * kStep + tid; r < rlen; r += kThreads) {
-    const int slot = r & (kRing - 1);
+  for (int r = (T - 1) * kStep + tid; r < rlen; r += K::NT) {
+    const int slot = r & (RING - 1);
     float v = 0.f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v += ring[k][slot];
+    for (int k = 0; k < 2 * NW; ++k) v += ring[k][slot];
     prow[r] = v;
   }
 
@@ -474,24 +492,24 @@ __global__ __launch_bounds__(kThreads, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ke
 }
 
 // ---------------------------------------------------------- backward: dK, dV
-template <int DP>
-__global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
+template <int DP, int NW>
+__global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H,
     int D, float c, float scale) {
   using G = Geo<DP>;
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[kStep * G::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Qt[G::DPV * kTLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Os[kStep * G::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ot[G::DPV * kTLD];
+  using K = Blk<NW>;
+  constexpr int CPT = (G::NCH + K::NT - 1) / K::NT;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[kStep * G::RLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Os[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) float Lq[kStep];
   __shared__ __attribute__((aligned(16))) float Dq[kStep];
-  __shared__ __attribute__((aligned(16))) float Bw[4 * kWLD];
+  __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int j_wg = blockIdx.x * kRows;
+  const int j_wg = blockIdx.x * K::ROWS;
   const int kk = wave * 32 + l32;
   const int kj = j_wg + kk;
   const bool kvalid = kj < S;
@@ -505,11 +523,10 @@ __global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_
   const float* pdh = pd + (int64_t)h * npd;
   const float* lse_bh = lse + (int64_t)bh * S;
   const float* dl_bh = delta_ws + (int64_t)bh * S;
+  const int c0 = 16 * ((lane >> 4) & 1);
 
-  for (int e = tid; e < (G::DPV - DP) * kTLD; e += kThreads) {
-    Qt[DP * kTLD + e] = 0;
-    Ot[DP * kTLD + e] = 0;
-  }
+  zero_pad_cols<DP, K::NT>(Qs);
+  zero_pad_cols<DP, K::NT>(Os);
 
   u32x4 kreg[G::KS], vreg[G::KS];
 #pragma unroll
@@ -526,34 +543,36 @@ __global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
-  u32x4 qst[G::CPT], ost[G::CPT];
-  float bst[kBPT];
+  u32x4 qst[CPT], ost[CPT];
+  float bst[K::BPT];
   float sst = 0.f;
   const int T = (S + kStep - 1) / kStep;
-  // Reversed window: copy cc, position y holds T[rb - (y - cc)], rb the
-  // largest diagonal of the iteration.
+  // Per-query statistics of the step: threads 0..63 lse, 64..127 delta.
   auto stats = [&](int i0) {
     const int q = i0 + (tid & 63);
     if (tid < 128) sst = q < S ? (tid < 64 ? lse_bh[q] : dl_bh[q]) : 0.f;
   };
-  load_tile<DP>(qst, qcol, ld, tok0, 0, S, D);
-  load_tile<DP>(ost, ocol, HD, tok0, 0, S, D);
-  load_bias(bst, pdh, npd, (j_wg + kRows - 1) - 0 + S - 1, -1);
+  // Reversed window: entry x holds T[rb - x], rb the largest diagonal of the step.
+  load_tile<DP, K::NT>(qst, qcol, ld, tok0, 0, S, D);
+  load_tile<DP, K::NT>(ost, ocol, HD, tok0, 0, S, D);
+  load_bias<NW>(bst, pdh, npd, (j_wg + K::ROWS - 1) - 0 + S - 1, -1);
   stats(0);
 
   for (int t = 0; t < T; ++t) {
     const int i0 = t * kStep;
     __syncthreads();
-    stash_tile<DP>(qst, Qs, Qt);
-    stash_tile<DP>(ost, Os, Ot);
-    stash_bias(bst, Bw);
-    if (tid < 64) Lq[tid] = sst;
-    else if (tid < 128) Dq[tid - 64] = sst;
+    stash_tile<DP, K::NT>(qst, Qs);
+    stash_tile<DP, K::NT>(ost, Os);
+    stash_bias<NW>(bst, Bw);
+    if (tid < 64)
+      Lq[tid] = sst;
+    else if (tid < 128)
+      Dq[tid - 64] = sst;
     __syncthreads();
     if (t + 1 < T) {
-      load_tile<DP>(qst, qcol, ld, tok0, i0 + kStep, S, D);
-      load_tile<DP>(ost, ocol, HD, tok0, i0 + kStep, S, D);
-      load_bias(bst, pdh, npd, (j_wg + kRows - 1) - (i0 + kStep) + S - 1, -1);
+      load_tile<DP, K::NT>(qst, qcol, ld, tok0, i0 + kStep, S, D);
+      load_tile<DP, K::NT>(ost, ocol, HD, tok0, i0 + kStep, S, D);
+      load_bias<NW>(bst, pdh, npd, (j_wg + K::ROWS - 1) - (i0 + kStep) + S - 1, -1);
       stats(i0 + kStep);
     }
     const bool tail = i0 + kStep > S;
@@ -564,11 +583,11 @@ __global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_
       for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < G::KS; ++s) {
-        acc = mfma32x32x16(ld16(Qs + (qb * 32 + l32) * G::KLD + 16 * s + 8 * g), kreg[s], acc);
-        accp = mfma32x32x16(ld16(Os + (qb * 32 + l32) * G::KLD + 16 * s + 8 * g), vreg[s], accp);
+        acc = mfma32x32x16(ld16(Qs + (qb * 32 + l32) * G::RLD + 16 * s + 8 * g), kreg[s], acc);
+        accp = mfma32x32x16(ld16(Os + (qb * 32 + l32) * G::RLD + 16 * s + 8 * g), vreg[s], accp);
       }
       float bias[16];
-      read_bias16(Bw, (kRows - 1) - kk + qb * 32 + 4 * g, bias);
+      read_bias16<NW>(Bw, (K::ROWS - 1) - kk + qb * 32 + 4 * g, bias);
       float p[16], ds[16];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
@@ -587,12 +606,11 @@ __global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_
       for (int u = 0; u < 2; ++u) {
         const u32x4 pa = pack8(&p[8 * u]);
         const u32x4 dsa = pack8(&ds[8 * u]);
+        const int k0 = qb * 32 + 16 * u + 4 * g;
 #pragma unroll
         for (int db = 0; db < G::DB; ++db) {
-          const int d = db * 32 + l32;
-          const int off = d * kTLD + perm_base(d, qb * 32 + 16 * u + 8 * g);
-          dv[db] = mfma32x32x16(pa, ld16(Ot + off), dv[db]);
-          dk[db] = mfma32x32x16(dsa, ld16(Qt + off), dk[db]);
+          dv[db] = mfma32x32x16(pa, tr_operand(Os, G::RLD, k0, k0 + 8, db * 32 + c0), dv[db]);
+          dk[db] = mfma32x32x16(dsa, tr_operand(Qs, G::RLD, k0, k0 + 8, db * 32 + c0), dk[db]);
         }
       }
     }
@@ -616,33 +634,39 @@ __global__ __launch_bounds__(kThreads, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_
   }
 }
 
-// dpd[h, k] = sum over b and 128-query blocks of the partial rows, fixed order.
+// dpd[h, k] = sum over b and query blocks of the partial rows, fixed order.
 // Block: 64 diagonals (lane) of head h; the 4 waves take every 4th (b, query
 // block) term, then the 4 wave sums are added in wave order.
-__global__ __launch_bounds__(kThreads) void relpos_dpd_reduce(const float* __restrict__ part,
-                                                              float* __restrict__ dpd, int B, int S,
-                                                              int H, int nqb) {
+__global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict__ part,
+                                                         float* __restrict__ dpd, int B, int S,
+                                                         int H, int nqb, int rows) {
   __shared__ float s[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + lane;
   const int h = blockIdx.y;
   const int npd = 2 * S - 1;
-  const int RS = S + 128;
-  const int rlen = S + kRows - 1;
+  const int RS = S + rows;
+  const int rlen = S + rows - 1;
   float acc = 0.f;
   if (k < npd) {
     const int terms = B * nqb;
 #pragma unroll 4
     for (int e = wave; e < terms; e += 4) {
       const int b = e / nqb, qb = e - b * nqb;
-      const int r = k - S + 128 + kRows * qb;
+      const int r = k - S + rows + rows * qb;
       if (r >= 0 && r < rlen) acc += part[((int64_t)(b * H + h) * nqb + qb) * RS + r];
     }
   }
   s[wave][lane] = acc;
   __syncthreads();
-  if (wave == 0 && k < npd) dpd[(int64_t)h * npd + k] = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
+  if (wave == 0 && k < npd)
+    dpd[(int64_t)h * npd + k] = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
 }
+
+// Waves per workgroup of the three attention kernels.
+constexpr int kFwdNW = 4;
+constexpr int kDqNW = 4;
+constexpr int kDkdvNW = 4;
 
 int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float scale) {
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return KRSI_ERR_BAD_SHAPE;
@@ -656,37 +680,42 @@ int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float sc
 
 int padded_dim(int D) { return (D + 15) / 16 * 16; }
 
+constexpr int kDqRows = Blk<kDqNW>::ROWS;
+
 size_t ws_delta_bytes(int B, int S, int H) { return align256((size_t)B * H * S * sizeof(float)); }
 size_t ws_part_bytes(int B, int S, int H) {
-  const size_t nqb = (size_t)ceil_div(S, kRows);
-  return align256((size_t)B * H * nqb * (size_t)(S + 128) * sizeof(float));
+  const size_t nqb = (size_t)ceil_div(S, kDqRows);
+  return align256((size_t)B * H * nqb * (size_t)(S + kDqRows) * sizeof(float));
 }
 
 template <int DP>
 void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* out32, float* lse,
                 int B, int S, int H, int D, float c, hipStream_t st) {
-  const dim3 grid((unsigned)ceil_div(S, kRows), (unsigned)(B * H));
-  hipLaunchKernelGGL(relpos_fwd_kernel<DP>, grid, dim3(kThreads), 0, st, (const uint16_t*)qkv, ld,
-                     pd, (uint16_t*)out, out32, lse, S, H, D, c);
+  using K = Blk<kFwdNW>;
+  const dim3 grid((unsigned)ceil_div(S, K::ROWS), (unsigned)(B * H));
+  hipLaunchKernelGGL((relpos_fwd_kernel<DP, kFwdNW>), grid, dim3(K::NT), 0, st,
+                     (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, c);
 }
 
 template <int DP>
 void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
                 const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S, int H,
                 int D, float c, float scale, hipStream_t st) {
+  using KQ = Blk<kDqNW>;
+  using KK = Blk<kDkdvNW>;
   float* delta = static_cast<float*>(ws);
   float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_delta_bytes(B, S, H));
-  const int nqb = (int)ceil_div(S, kRows);
-  const dim3 grid((unsigned)nqb, (unsigned)(B * H));
-  hipLaunchKernelGGL(relpos_bwd_dq_kernel<DP>, grid, dim3(kThreads), 0, st, (const uint16_t*)qkv,
-                     ld, pd, (const uint16_t*)dout, out32, lse, delta, part, (uint16_t*)dqkv, ldd,
-                     S, H, D, c, scale);
-  hipLaunchKernelGGL(relpos_bwd_dkdv_kernel<DP>, grid, dim3(kThreads), 0, st,
-                     (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
-                     (const float*)delta, (uint16_t*)dqkv, ldd, S, H, D, c, scale);
+  const int nqb = (int)ceil_div(S, KQ::ROWS);
+  hipLaunchKernelGGL((relpos_bwd_dq_kernel<DP, kDqNW>), dim3((unsigned)nqb, (unsigned)(B * H)),
+                     dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
+                     lse, delta, part, (uint16_t*)dqkv, ldd, S, H, D, c, scale);
+  hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DP, kDkdvNW>),
+                     dim3((unsigned)ceil_div(S, KK::ROWS), (unsigned)(B * H)), dim3(KK::NT), 0, st,
+                     (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse, (const float*)delta,
+                     (uint16_t*)dqkv, ldd, S, H, D, c, scale);
   const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
-  hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(kThreads), 0, st, (const float*)part, dpd, B,
-                     S, H, nqb);
+  hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S, H,
+                     nqb, KQ::ROWS);
 }
 
 }  // namespace
