@@ -77,6 +77,7 @@ struct Blk {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) float lds_f32;
 
 constexpr u32x4 kZero4 = {0u, 0u, 0u, 0u};
 
@@ -177,6 +178,73 @@ __device__ __forceinline__ void read_bias16(const float* bw, int x0, float* out)
 }
 
 // ------------------------------------------------------------------- forward
+// One 64-key step of the forward for this lane's query: scores, exact running max,
+// p = exp2(s - m), l += p, O^T += V^T P^T. TAIL masks keys >= S (last step only).
+template <int DP, int NW, bool TAIL>
+__device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
+                                         const u32x4* qreg, f32x16* oacc, float& m_run, float& l_run,
+                                         int j0, int S, int ii, int g, int l32, int c0, float c) {
+  using G = Geo<DP>;
+  using K = Blk<NW>;
+  float sc[2][16];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < G::KS; ++s)
+      acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
+    float bias[16];
+    read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii, bias);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[kb][r] = acc[r] * c + bias[r];
+    if (TAIL) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sc[kb][r] = -INFINITY;
+    }
+  }
+  float mx = sc[0][0];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  // Exact running max, as the reference (relpos_attention.py:48-50): the step's largest
+  // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
+  // some lane's max moved.
+  const bool need = mx > m_run;
+  if (__any(need)) {
+    const float mnew = need ? mx : m_run;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+    m_run = mnew;
+  }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = __builtin_amdgcn_exp2f(sc[kb][r] - m_run);
+      l_run += p;
+      sc[kb][r] = p;
+    }
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const u32x4 pb = pack8(&sc[kb][8 * u]);
+      const int k0 = kb * 32 + 16 * u + 4 * g;
+#pragma unroll
+      for (int db = 0; db < G::DB; ++db)
+        oacc[db] = mfma32x32x16(tr_operand(Vs, G::RLD, k0, k0 + 8, db * 32 + c0), pb, oacc[db]);
+    }
+}
+
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
@@ -227,7 +295,8 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
   load_tile<DP, K::NT>(vst, vcol, ld, tok0, 0, S, D);
   load_bias<NW>(bst, pdh, npd, 0 - i_wg - (K::ROWS - 1) + S - 1, 1);
 
-  for (int t = 0; t < T; ++t) {
+  // Stage step t (stash the prefetched tile, then prefetch step t+1).
+  auto stage = [&](int t) {
     const int j0 = t * kStep;
     __syncthreads();
     stash_tile<DP, K::NT>(kst, Ks);
@@ -239,66 +308,17 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
       load_tile<DP, K::NT>(vst, vcol, ld, tok0, j0 + kStep, S, D);
       load_bias<NW>(bst, pdh, npd, j0 + kStep - i_wg - (K::ROWS - 1) + S - 1, 1);
     }
-
-    float sc[2][16];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x16 acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-#pragma unroll
-      for (int s = 0; s < G::KS; ++s)
-        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
-      float bias[16];
-      read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii, bias);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sc[kb][r] = acc[r] * c + bias[r];
-    }
-    if (j0 + kStep > S) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sc[kb][r] = -INFINITY;
-    }
-    float mx = sc[0][0];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Exact running max, as the reference (relpos_attention.py:48-50): the step's largest
-    // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
-    // some lane's max moved.
-    const bool need = mx > m_run;
-    if (__any(need)) {
-      const float mnew = need ? mx : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < G::DB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-      m_run = mnew;
-    }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(sc[kb][r] - m_run);
-        l_run += p;
-        sc[kb][r] = p;
-      }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const u32x4 pb = pack8(&sc[kb][8 * u]);
-        const int k0 = kb * 32 + 16 * u + 4 * g;
-#pragma unroll
-        for (int db = 0; db < G::DB; ++db)
-          oacc[db] = mfma32x32x16(tr_operand(Vs, G::RLD, k0, k0 + 8, db * 32 + c0), pb, oacc[db]);
-      }
+  };
+  // Full 64-key steps carry no key mask; a partial last step (S % 64 != 0) runs once after
+  // the loop, so the loop body holds a single copy of the step.
+  const int Tfull = S / kStep;
+  for (int t = 0; t < Tfull; ++t) {
+    stage(t);
+    fwd_step<DP, NW, false>(Ks, Vs, Bw, qreg, oacc, m_run, l_run, t * kStep, S, ii, g, l32, c0, c);
+  }
+  if (Tfull < T) {
+    stage(Tfull);
+    fwd_step<DP, NW, true>(Ks, Vs, Bw, qreg, oacc, m_run, l_run, Tfull * kStep, S, ii, g, l32, c0, c);
   }
 
   const float l = l_run + __shfl_xor(l_run, 32);
@@ -325,6 +345,78 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
 }
 
 // ------------------------------------------------ backward: delta, dQ and dpd
+// Diagonal ring of the dQ kernel: RING slots indexed by diagonal mod RING, plus a
+// 32-slot overflow zone that aliases slots 0..31, so the 16 updates of one D tile
+// (diagonals base + 8a + b, a, b < 4) use one base register and immediate offsets.
+// Folding a diagonal reads (and clears) both of its slots.
+template <int NW>
+__device__ __forceinline__ float ring_take(float (*ring)[Blk<NW>::RING + 32], int slot, bool clear) {
+  constexpr int RING = Blk<NW>::RING;
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < 2 * NW; ++k) {
+    v += ring[k][slot];
+    if (clear) ring[k][slot] = 0.f;
+    if (slot < 32) {
+      v += ring[k][slot + RING];
+      if (clear) ring[k][slot + RING] = 0.f;
+    }
+  }
+  return v;
+}
+
+// One 64-key step of the dQ kernel for this lane's query: p = exp2(s - lse),
+// ds = p (dp - delta), ds into the diagonal ring, dQ^T += K^T dS^T. Invalid
+// query lanes carry lse = +inf, so their p is 0 without a mask; TAIL masks keys
+// >= S (last step only).
+template <int DP, int NW, bool TAIL>
+__device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
+                                        float* myring, const u32x4* qreg, const u32x4* doreg,
+                                        f32x16* dq, float lse_q, float delta, int j0, int S, int ii,
+                                        int g, int l32, int c0, float c) {
+  using G = Geo<DP>;
+  using K = Blk<NW>;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    f32x16 acc, accp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < G::KS; ++s) {
+      acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
+      accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), doreg[s], accp);
+    }
+    float bias[16];
+    const int x0 = kb * 32 + 4 * g + (K::ROWS - 1) - ii;
+    read_bias16<NW>(Bw, x0, bias);
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - lse_q);
+      if (TAIL && j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
+      ds[r] = p * (accp[r] - delta);
+    }
+    // Diagonal of D-register r: j - i + ROWS - 1 - i_wg = j0 + x0 + 8a + b. Within one
+    // register the 32 lanes of a half hit 32 distinct diagonals of their own ring, and LDS
+    // operations of a wave complete in order, so a plain read-modify-write per register is
+    // exact (LDS float atomics cost ~30x more here). Lanes ii and ii+1 reach the same
+    // diagonal through neighbouring registers, so the read-modify-writes must stay in
+    // register order: the accesses are volatile, which forbids batching the reads ahead of
+    // the writes (the compiler only sees that one lane's 16 slots are distinct).
+    volatile lds_f32* rp = (volatile lds_f32*)myring + ((j0 + x0) & (K::RING - 1));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) rp[8 * (r >> 2) + (r & 3)] = rp[8 * (r >> 2) + (r & 3)] + ds[r];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const u32x4 dsb = pack8(&ds[8 * u]);
+      const int k0 = kb * 32 + 16 * u + 4 * g;
+#pragma unroll
+      for (int db = 0; db < G::DB; ++db)
+        dq[db] = mfma32x32x16(tr_operand(Ks, G::RLD, k0, k0 + 8, db * 32 + c0), dsb, dq[db]);
+    }
+  }
+}
+
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
@@ -338,7 +430,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
-  __shared__ float ring[2 * NW][RING];
+  __shared__ float ring[2 * NW][RING + 32];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
@@ -359,7 +451,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   const int c0 = 16 * ((lane >> 4) & 1);
 
   zero_pad_cols<DP, K::NT>(Ks);
-  for (int e = tid; e < 2 * NW * RING; e += K::NT) (&ring[0][0])[e] = 0.f;
+  for (int e = tid; e < 2 * NW * (RING + 32); e += K::NT) (&ring[0][0])[e] = 0.f;
 
   // Register-resident operands and per-query statistics.
   u32x4 qreg[G::KS], doreg[G::KS];
@@ -383,7 +475,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     }
   }
   const float delta = dsum + __shfl_xor(dsum, 32);
-  const float lse_q = qvalid ? lse[(int64_t)bh * S + qi] : 0.f;
+  // +inf makes p = exp2(s - lse) exactly 0 on lanes past S (their s is finite).
+  const float lse_q = qvalid ? lse[(int64_t)bh * S + qi] : INFINITY;
   if (qvalid && g == 0) delta_ws[(int64_t)bh * S + qi] = delta;
 
   f32x16 dq[G::DB];
@@ -400,7 +493,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   load_tile<DP, K::NT>(vst, vcol, ld, tok0, 0, S, D);
   load_bias<NW>(bst, pdh, npd, 0 - i_wg - (K::ROWS - 1) + S - 1, 1);
 
-  for (int t = 0; t < T; ++t) {
+  // Stage step t (stash the prefetched tile, prefetch step t+1, fold finished diagonals).
+  auto stage = [&](int t) {
     const int j0 = t * kStep;
     __syncthreads();
     stash_tile<DP, K::NT>(kst, Ks);
@@ -416,63 +510,24 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     // iteration t-1: fold the rings in order into the partial row.
     if (t > 0 && wave == 0) {
       const int r = (t - 1) * kStep + lane;
-      const int slot = r & (RING - 1);
-      float v = 0.f;
-#pragma unroll
-      for (int k = 0; k < 2 * NW; ++k) {
-        v += ring[k][slot];
-        ring[k][slot] = 0.f;
-      }
-      prow[r] = v;
+      prow[r] = ring_take<NW>(ring, r & (RING - 1), true);
     }
-
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x16 acc, accp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
-#pragma unroll
-      for (int s = 0; s < G::KS; ++s) {
-        acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
-        accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), doreg[s], accp);
-      }
-      float bias[16];
-      const int x0 = kb * 32 + 4 * g + (K::ROWS - 1) - ii;
-      read_bias16<NW>(Bw, x0, bias);
-      const bool tail = j0 + kStep > S;
-      float ds[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - lse_q);
-        if (!qvalid) p = 0.f;
-        if (tail && j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
-        ds[r] = p * (accp[r] - delta);
-      }
-      // Diagonal of D-register r: j - i + ROWS - 1 - i_wg = 64t + x0 + 8a + b. Within one
-      // register the 32 lanes of a half hit 32 distinct slots of their own ring, and LDS
-      // operations of a wave complete in order, so a plain read-modify-write is exact
-      // (LDS float atomics cost ~30x more here).
-#pragma unroll
-      for (int r = 0; r < 16; ++r) myring[(j0 + x0 + 8 * (r >> 2) + (r & 3)) & (RING - 1)] += ds[r];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const u32x4 dsb = pack8(&ds[8 * u]);
-        const int k0 = kb * 32 + 16 * u + 4 * g;
-#pragma unroll
-        for (int db = 0; db < G::DB; ++db)
-          dq[db] = mfma32x32x16(tr_operand(Ks, G::RLD, k0, k0 + 8, db * 32 + c0), dsb, dq[db]);
-      }
-    }
+  };
+  // Full 64-key steps carry no key mask; a partial last step runs once after the loop.
+  const int Tfull = S / kStep;
+  for (int t = 0; t < Tfull; ++t) {
+    stage(t);
+    dq_step<DP, NW, false>(Ks, Vs, Bw, myring, qreg, doreg, dq, lse_q, delta, t * kStep, S, ii, g,
+                           l32, c0, c);
+  }
+  if (Tfull < T) {
+    stage(Tfull);
+    dq_step<DP, NW, true>(Ks, Vs, Bw, myring, qreg, doreg, dq, lse_q, delta, Tfull * kStep, S, ii,
+                          g, l32, c0, c);
   }
 
   __syncthreads();
-  for (int r = (T - 1) * kStep + tid; r < rlen; r += K::NT) {
-    const int slot = r & (RING - 1);
-    float v = 0.f;
-#pragma unroll
-    for (int k = 0; k < 2 * NW; ++k) v += ring[k][slot];
-    prow[r] = v;
-  }
+  for (int r = (T - 1) * kStep + tid; r < rlen; r += K::NT) prow[r] = ring_take<NW>(ring, r & (RING - 1), false);
 
   if (qvalid) {
     const int64_t qbase = (tok0 + qi) * ldd + (int64_t)h * D;
@@ -547,10 +602,11 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   float bst[K::BPT];
   float sst = 0.f;
   const int T = (S + kStep - 1) / kStep;
-  // Per-query statistics of the step: threads 0..63 lse, 64..127 delta.
+  // Per-query statistics of the step: threads 0..63 lse, 64..127 delta. Rows past S get
+  // lse = +inf, which makes their p = exp2(s - lse) exactly 0 (s is finite there).
   auto stats = [&](int i0) {
     const int q = i0 + (tid & 63);
-    if (tid < 128) sst = q < S ? (tid < 64 ? lse_bh[q] : dl_bh[q]) : 0.f;
+    if (tid < 128) sst = q < S ? (tid < 64 ? lse_bh[q] : dl_bh[q]) : (tid < 64 ? INFINITY : 0.f);
   };
   // Reversed window: entry x holds T[rb - x], rb the largest diagonal of the step.
   load_tile<DP, K::NT>(qst, qcol, ld, tok0, 0, S, D);
@@ -575,7 +631,6 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       load_bias<NW>(bst, pdh, npd, (j_wg + K::ROWS - 1) - (i0 + kStep) + S - 1, -1);
       stats(i0 + kStep);
     }
-    const bool tail = i0 + kStep > S;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       f32x16 acc, accp;
@@ -596,8 +651,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 #pragma unroll
         for (int b4 = 0; b4 < 4; ++b4) {
           const int r = 4 * a + b4;
-          float pv = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - l4[b4]);
-          if (tail && i0 + qb * 32 + 8 * a + 4 * g + b4 >= S) pv = 0.f;
+          const float pv = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - l4[b4]);
           p[r] = pv;
           ds[r] = pv * (accp[r] - d4[b4]);
         }
