@@ -85,7 +85,10 @@ int krsi_geglu_bwd_bf16(const void* g, const void* u, void* du, int64_t rows, in
  * out: [B*S, H*D] bf16; out32: same, fp32; lse: [B*H, S] fp32 in the log2
  *      domain (lse = log2 sum_j 2^{(q.k*scale + bias) * log2(e)}).
  * Limits: D % 8 == 0 and 8 <= D <= 128, ld_qkv % 8 == 0, ld_qkv >= 3*H*D,
- *         S >= 1, scale finite and > 0. Non-causal.                         */
+ *         S >= 1, S * ld_qkv * 2 < 2^31 bytes (UNSUPPORTED otherwise),
+ *         scale finite, and scale == 0 or |scale| * log2(e) >= 2^-60
+ *         (BAD_SCALE otherwise: the bias is folded into the score accumulator
+ *         as pd * log2(e) / |scale * log2(e)|). Non-causal.                  */
 int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void* out,
                          float* out32, float* lse, int32_t B, int32_t S, int32_t H,
                          int32_t D, float scale, void* stream);

@@ -16,12 +16,15 @@
 //     workgroup of NW wavefronts owns 32*NW. The register-resident side (Q and
 //     dO, or K and V) is loaded once from HBM with 128-bit loads straight into
 //     MFMA operand registers.
-//   * The streamed side (64 positions per step) is staged in LDS row-major
-//     with 128-bit writes only. Products that contract over the head dim read
-//     it with 128-bit row reads; products that contract over positions read it
-//     with ds_read_b64_tr_b16, which returns, per lane, 4 consecutive rows of
-//     one column of a 4x16 block, so no transposed copy is ever written.
-//     Global loads of step t+1 are issued before the MFMAs of step t.
+//   * The streamed side (64 positions per step) is fetched with raw buffer
+//     loads whose resource ends at the last valid row of the (batch, head), so
+//     rows past S and head-dim padding read as zero in hardware with no
+//     per-element mask; loads of step t+1 are issued before the MFMAs of step t.
+//     It is staged in LDS row-major with 128-bit writes only. Products that
+//     contract over the head dim read it with 128-bit row reads; products that
+//     contract over positions read it with ds_read_b64_tr_b16, which returns,
+//     per lane, 4 consecutive rows of one column of a 4x16 block, so no
+//     transposed copy is ever written.
 //   * Scores are computed transposed (S^T = K Q^T) in the forward and dQ
 //     kernels, so each lane owns one query: the row max and row sum are in-lane
 //     reductions plus one cross-half exchange, and lse/delta are registers.
@@ -29,13 +32,18 @@
 //     MFMA: registers 8u..8u+7 of half-wave g hold positions 16u + 4g + {0..3}
 //     and 16u + 8 + 4g + {0..3}, exactly the two 4-row groups two transposed
 //     reads return, so the K order of both operands agrees without shuffles.
+//   * The bias is folded into the score MFMA: with c = |scale| log2(e) the
+//     accumulator starts at pd * log2(e) / c and the exponent is one fma,
+//     exp2(acc * c - m). A negative scale flips the sign bits of the
+//     register-resident bf16 operand (exact); scale 0 zeroes it (c = 1).
 //   * The Toeplitz bias of a (32*NW) x 64 tile is a window of consecutive table
-//     entries, staged once per step (times log2 e) in 4 copies shifted by one
-//     entry, so every lane reads its 4 consecutive entries with one aligned
-//     128-bit LDS read.
+//     entries, staged once per step in 4 copies shifted by one entry, so every
+//     lane reads its 4 consecutive entries with one aligned 128-bit LDS read;
+//     the copy stride puts the 8 lanes of one read phase on distinct banks.
 //   * Online softmax keeps the exact running max per 64-key step (the step
 //     maximum gives p = 1, exact in bf16, as in the reference); the fp32
-//     accumulators are rescaled only when some lane's max moved.
+//     accumulators are rescaled only when some lane's max moved. The row sum
+//     adds the bf16 p the PV product uses (v_dot2c_f32_bf16, two per op).
 //   * dpd is reduced along the diagonals j - i inside the dQ kernel: each
 //     (wave, half-wave) adds its fp32 ds into a private LDS ring indexed by
 //     diagonal. Within one register the 32 lanes of a half-wave hit distinct
@@ -69,10 +77,19 @@ template <int NW>
 struct Blk {
   static constexpr int ROWS = 32 * NW;             // queries or keys per workgroup
   static constexpr int NT = 64 * NW;               // threads per workgroup
-  static constexpr int WLD = ROWS + kStep + 4;     // bias copy length (multiple of 4)
+  static constexpr int WLD = ROWS + kStep + 8;     // bias copy stride, = 8 (mod 32) floats
   static constexpr int WIN = WLD - 3;              // distinct window entries loaded
   static constexpr int BPT = (WIN + NT - 1) / NT;  // window entries per thread
   static constexpr int RING = ROWS <= 128 ? 256 : 512;  // dpd ring (>= ROWS + 2 * kStep - 1)
+};
+
+// Scale folding: scores are acc * c with acc = q'.k + pd * bmul, q' = (q & qand) ^ qxor
+// on the register-resident bf16 operand.
+struct Fold {
+  float c;        // |scale| * log2(e), or 1 when scale == 0
+  float bmul;     // log2(e) / c
+  uint32_t qand;  // 0 when scale == 0
+  uint32_t qxor;  // bf16 sign bits when scale < 0
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -82,6 +99,38 @@ typedef __attribute__((address_space(3))) float lds_f32;
 constexpr u32x4 kZero4 = {0u, 0u, 0u, 0u};
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+__device__ __forceinline__ u32x4 fold_operand(u32x4 v, const Fold& f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (v[i] & f.qand) ^ f.qxor;
+  return v;
+}
+
+// Raw buffer resources (gfx9 descriptor word 3): a load whose byte offset is at or
+// past num_records returns zero. kOob is past every resource built here (the
+// launchers keep them below 2^31 bytes).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr uint32_t kOob = 0x80000000u;
+
+// The whole byte offset must reach the instruction in the VGPR: the range check is
+// made on the VGPR offset, so a constant the compiler split off into the immediate
+// field would turn a valid offset whose variable part is negative into a zero read.
+// An empty asm makes the offset opaque, so no constant can be split off.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0));
+}
+__device__ __forceinline__ float bload4(rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0));
+}
 
 // MFMA operand whose 8 K values are rows [k0, k0+4) and [k1, k1+4) of column
 // c0 + (lane % 16) of a row-major LDS tile (stride ld): two transposed reads,
@@ -97,28 +146,40 @@ __device__ __forceinline__ u32x4 tr_operand(const uint16_t* tile, int ld, int k0
   return u32x4{ua.x, ua.y, ub.x, ub.y};
 }
 
-// Load one streamed tile (rows p0..p0+63 of a [*, ld] bf16 matrix whose
-// column block starts at `col`) into registers, zero outside [0, S) x [0, D).
+// Streamed tiles. Chunk c = threadIdx.x + k * NT of a tile is row c / CPR, head-dim
+// columns d0 = 8 (c % CPR) .. +7. Its byte offset from the tile's first row is fixed
+// per thread; chunks past D (or past the tile) get kOob and read as zero.
 template <int DP, int NT>
-__device__ __forceinline__ void load_tile(u32x4* regs, const uint16_t* col, int64_t ld, int64_t tok0,
-                                          int p0, int S, int D) {
+struct Tile {
+  static constexpr int CPT = (Geo<DP>::NCH + NT - 1) / NT;
+};
+
+template <int DP, int NT>
+__device__ __forceinline__ void tile_offsets(uint32_t* voff, int64_t ld, int D) {
   using G = Geo<DP>;
-  constexpr int CPT = (G::NCH + NT - 1) / NT;
 #pragma unroll
-  for (int k = 0; k < CPT; ++k) {
+  for (int k = 0; k < Tile<DP, NT>::CPT; ++k) {
     const int c = threadIdx.x + k * NT;
     const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
-    const bool ok = c < G::NCH && p0 + row < S && d0 < D;
-    regs[k] = ok ? ld16(col + (tok0 + p0 + row) * ld + d0) : kZero4;
+    voff[k] = opaque((c < G::NCH && d0 < D) ? (uint32_t)(row * ld + d0) * 2u : kOob);
   }
+}
+
+// Rows p0..p0+63 of the [S, D] slice whose row 0 is `origin` (row stride ld): the
+// resource ends at the last byte of row S-1, so rows >= S read as zero.
+template <int DP, int NT>
+__device__ __forceinline__ void load_tile(u32x4* regs, const uint32_t* voff, const uint16_t* origin,
+                                          int64_t ld, int p0, int S, int D) {
+  const rsrc_t r = make_rsrc(origin + (int64_t)p0 * ld, (uint32_t)(((int64_t)(S - 1 - p0) * ld + D) * 2));
+#pragma unroll
+  for (int k = 0; k < Tile<DP, NT>::CPT; ++k) regs[k] = bload16(r, voff[k]);
 }
 
 template <int DP, int NT>
 __device__ __forceinline__ void stash_tile(const u32x4* regs, uint16_t* tile) {
   using G = Geo<DP>;
-  constexpr int CPT = (G::NCH + NT - 1) / NT;
 #pragma unroll
-  for (int k = 0; k < CPT; ++k) {
+  for (int k = 0; k < Tile<DP, NT>::CPT; ++k) {
     const int c = threadIdx.x + k * NT;
     if (c < G::NCH) {
       const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
@@ -137,16 +198,18 @@ __device__ __forceinline__ void zero_pad_cols(uint16_t* tile) {
     for (int e = threadIdx.x; e < kStep * W; e += NT) tile[(e / W) * G::RLD + DP + e % W] = 0;
 }
 
-// Bias window entry x (0 <= x < WIN) holds T[wb + sgn * x] * log2(e), zero
-// outside [0, 2S - 1); it is stored at position x + cc of copy cc.
+// Bias window entry x (0 <= x < WIN) holds T[wb + sgn * x] * bmul, zero outside
+// [0, 2S - 1) (out-of-range offsets, negative ones included, fall past the
+// resource); it is stored at position x + cc of copy cc.
 template <int NW>
-__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn) {
+__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn,
+                                          float bmul) {
   using K = Blk<NW>;
+  const rsrc_t r = make_rsrc(pdh, (uint32_t)npd * 4u);
 #pragma unroll
   for (int k = 0; k < K::BPT; ++k) {
     const int x = threadIdx.x + k * K::NT;
-    const int src = wb + sgn * x;
-    regs[k] = (x < K::WIN && src >= 0 && src < npd) ? pdh[src] * kLog2e : 0.f;
+    regs[k] = x < K::WIN ? bload4(r, opaque((uint32_t)(wb + sgn * x) * 4u)) * bmul : 0.f;
   }
 }
 
@@ -163,54 +226,58 @@ __device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
   }
 }
 
-// The 16 bias values of one 32x32 D tile: window entries x0 + 8a + b
-// (a, b = 0..3), read from the copy that makes x0 16-byte aligned.
+// The 16 bias values of one 32x32 D tile, as the tile's initial accumulator:
+// window entries x0 + 8a + b (a, b = 0..3), read from the copy that makes x0
+// 16-byte aligned.
 template <int NW>
-__device__ __forceinline__ void read_bias16(const float* bw, int x0, float* out) {
+__device__ __forceinline__ f32x16 read_bias16(const float* bw, int x0) {
   const int cc = (-x0) & 3;
   const float* p = bw + cc * Blk<NW>::WLD + x0 + cc;
+  f32x16 out;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
     const f32x4 v = *reinterpret_cast<const f32x4*>(p + 8 * a);
 #pragma unroll
     for (int b = 0; b < 4; ++b) out[4 * a + b] = v[b];
   }
+  return out;
+}
+
+// Row sum of bf16 p values: two per v_dot2c_f32_bf16 against (1, 1).
+__device__ __forceinline__ float add_bf16_pair(uint32_t pair, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
 }
 
 // ------------------------------------------------------------------- forward
-// One 64-key step of the forward for this lane's query: scores, exact running max,
-// p = exp2(s - m), l += p, O^T += V^T P^T. TAIL masks keys >= S (last step only).
+// One 64-key step of the forward for this lane's query: scores (bias folded into
+// the accumulator), exact running max, p = exp2(acc c - m), l += bf16(p),
+// O^T += V^T P^T. TAIL masks keys >= S (last step only).
 template <int DP, int NW, bool TAIL>
 __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
-                                         const u32x4* qreg, f32x16* oacc, float& m_run, float& l_run,
+                                         const u32x4* qreg, f32x16* oacc, float& m_run, float* l_run,
                                          int j0, int S, int ii, int g, int l32, int c0, float c) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  float sc[2][16];
+  f32x16 sc[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    f32x16 acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    sc[kb] = read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii);
 #pragma unroll
     for (int s = 0; s < G::KS; ++s)
-      acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
-    float bias[16];
-    read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii, bias);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sc[kb][r] = acc[r] * c + bias[r];
+      sc[kb] = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], sc[kb]);
     if (TAIL) {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sc[kb][r] = -INFINITY;
     }
   }
-  float mx = sc[0][0];
+  float mx = fmaxf(sc[0][0], sc[1][0]);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
   // Exact running max, as the reference (relpos_attention.py:48-50): the step's largest
   // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
   // some lane's max moved.
@@ -218,41 +285,41 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
   if (__any(need)) {
     const float mnew = need ? mx : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
-    l_run *= alpha;
+    l_run[0] *= alpha;
+    l_run[1] *= alpha;
 #pragma unroll
     for (int db = 0; db < G::DB; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
     m_run = mnew;
   }
+  const float negm = -m_run;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < 2; ++kb) {
+    float p[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = __builtin_amdgcn_exp2f(sc[kb][r] - m_run);
-      l_run += p;
-      sc[kb][r] = p;
-    }
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+    for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][r], c, negm));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const u32x4 pb = pack8(&sc[kb][8 * u]);
+      const u32x4 pb = pack8(&p[8 * u]);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) l_run[w & 1] = add_bf16_pair(pb[w], l_run[w & 1]);
       const int k0 = kb * 32 + 16 * u + 4 * g;
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
         oacc[db] = mfma32x32x16(tr_operand(Vs, G::RLD, k0, k0 + 8, db * 32 + c0), pb, oacc[db]);
     }
+  }
 }
 
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
-    int D, float c) {
+    int D, Fold f) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int CPT = (G::NCH + K::NT - 1) / K::NT;
+  constexpr int CPT = Tile<DP, K::NT>::CPT;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
@@ -265,12 +332,13 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
   const bool qvalid = qi < S;
   const int64_t tok0 = (int64_t)b * S;
   const int64_t HD = (int64_t)H * D;
-  const uint16_t* qcol = qkv + (int64_t)h * D;
-  const uint16_t* kcol = qkv + HD + (int64_t)h * D;
-  const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
+  const uint16_t* q0 = qkv + tok0 * ld + (int64_t)h * D;  // row 0 of this (batch, head)'s Q
+  const uint16_t* k0p = q0 + HD;
+  const uint16_t* v0p = q0 + 2 * HD;
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
   const int c0 = 16 * ((lane >> 4) & 1);
+  const float c = f.c;
 
   zero_pad_cols<DP, K::NT>(Vs);
 
@@ -278,7 +346,7 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
 #pragma unroll
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
-    qreg[s] = (qvalid && d0 < D) ? ld16(qcol + (tok0 + qi) * ld + d0) : kZero4;
+    qreg[s] = (qvalid && d0 < D) ? fold_operand(ld16(q0 + (int64_t)qi * ld + d0), f) : kZero4;
   }
 
   f32x16 oacc[G::DB];
@@ -286,27 +354,31 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
   for (int db = 0; db < G::DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = -INFINITY, l_run[2] = {0.f, 0.f};
 
+  uint32_t voff[CPT];
+  tile_offsets<DP, K::NT>(voff, ld, D);
   u32x4 kst[CPT], vst[CPT];
   float bst[K::BPT];
   const int T = (S + kStep - 1) / kStep;
-  load_tile<DP, K::NT>(kst, kcol, ld, tok0, 0, S, D);
-  load_tile<DP, K::NT>(vst, vcol, ld, tok0, 0, S, D);
-  load_bias<NW>(bst, pdh, npd, 0 - i_wg - (K::ROWS - 1) + S - 1, 1);
+  // Window base of step t: entry x is table index wb + x, wb = j0 - i_wg - (ROWS-1) + S-1.
+  const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
+  load_tile<DP, K::NT>(kst, voff, k0p, ld, 0, S, D);
+  load_tile<DP, K::NT>(vst, voff, v0p, ld, 0, S, D);
+  load_bias<NW>(bst, pdh, npd, wb0, 1, f.bmul);
 
   // Stage step t (stash the prefetched tile, then prefetch step t+1).
   auto stage = [&](int t) {
-    const int j0 = t * kStep;
+    const int j1 = (t + 1) * kStep;
     __syncthreads();
     stash_tile<DP, K::NT>(kst, Ks);
     stash_tile<DP, K::NT>(vst, Vs);
     stash_bias<NW>(bst, Bw);
     __syncthreads();
     if (t + 1 < T) {
-      load_tile<DP, K::NT>(kst, kcol, ld, tok0, j0 + kStep, S, D);
-      load_tile<DP, K::NT>(vst, vcol, ld, tok0, j0 + kStep, S, D);
-      load_bias<NW>(bst, pdh, npd, j0 + kStep - i_wg - (K::ROWS - 1) + S - 1, 1);
+      load_tile<DP, K::NT>(kst, voff, k0p, ld, j1, S, D);
+      load_tile<DP, K::NT>(vst, voff, v0p, ld, j1, S, D);
+      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, f.bmul);
     }
   };
   // Full 64-key steps carry no key mask; a partial last step (S % 64 != 0) runs once after
@@ -321,7 +393,8 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     fwd_step<DP, NW, true>(Ks, Vs, Bw, qreg, oacc, m_run, l_run, Tfull * kStep, S, ii, g, l32, c0, c);
   }
 
-  const float l = l_run + __shfl_xor(l_run, 32);
+  const float lh = l_run[0] + l_run[1];
+  const float l = lh + __shfl_xor(lh, 32);
   if (qvalid) {
     const int64_t obase = (tok0 + qi) * HD + (int64_t)h * D;
 #pragma unroll
@@ -365,34 +438,32 @@ __device__ __forceinline__ float ring_take(float (*ring)[Blk<NW>::RING + 32], in
   return v;
 }
 
-// One 64-key step of the dQ kernel for this lane's query: p = exp2(s - lse),
+// One 64-key step of the dQ kernel for this lane's query: p = exp2(acc c - lse),
 // ds = p (dp - delta), ds into the diagonal ring, dQ^T += K^T dS^T. Invalid
 // query lanes carry lse = +inf, so their p is 0 without a mask; TAIL masks keys
 // >= S (last step only).
 template <int DP, int NW, bool TAIL>
 __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
                                         float* myring, const u32x4* qreg, const u32x4* doreg,
-                                        f32x16* dq, float lse_q, float delta, int j0, int S, int ii,
+                                        f32x16* dq, float neg_lse, float delta, int j0, int S, int ii,
                                         int g, int l32, int c0, float c) {
   using G = Geo<DP>;
   using K = Blk<NW>;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    f32x16 acc, accp;
+    const int x0 = kb * 32 + 4 * g + (K::ROWS - 1) - ii;
+    f32x16 acc = read_bias16<NW>(Bw, x0), accp;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
+    for (int r = 0; r < 16; ++r) accp[r] = 0.f;
 #pragma unroll
     for (int s = 0; s < G::KS; ++s) {
       acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
       accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), doreg[s], accp);
     }
-    float bias[16];
-    const int x0 = kb * 32 + 4 * g + (K::ROWS - 1) - ii;
-    read_bias16<NW>(Bw, x0, bias);
     float ds[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      float p = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - lse_q);
+      float p = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], c, neg_lse));
       if (TAIL && j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
       ds[r] = p * (accp[r] - delta);
     }
@@ -422,10 +493,10 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ out32,
     const float* __restrict__ lse, float* __restrict__ delta_ws, float* __restrict__ part,
-    uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H, int D, float c, float scale) {
+    uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H, int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int CPT = (G::NCH + K::NT - 1) / K::NT;
+  constexpr int CPT = Tile<DP, K::NT>::CPT;
   constexpr int RING = K::RING;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
@@ -440,15 +511,16 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   const bool qvalid = qi < S;
   const int64_t tok0 = (int64_t)b * S;
   const int64_t HD = (int64_t)H * D;
-  const uint16_t* qcol = qkv + (int64_t)h * D;
-  const uint16_t* kcol = qkv + HD + (int64_t)h * D;
-  const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
+  const uint16_t* q0 = qkv + tok0 * ld + (int64_t)h * D;
+  const uint16_t* k0p = q0 + HD;
+  const uint16_t* v0p = q0 + 2 * HD;
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
   const int RS = S + K::ROWS;         // partial row stride
   const int rlen = S + K::ROWS - 1;   // diagonals one query block touches
   float* prow = part + ((int64_t)bh * gridDim.x + blockIdx.x) * RS;
   const int c0 = 16 * ((lane >> 4) & 1);
+  const float c = f.c;
 
   zero_pad_cols<DP, K::NT>(Ks);
   for (int e = tid; e < 2 * NW * (RING + 32); e += K::NT) (&ring[0][0])[e] = 0.f;
@@ -461,7 +533,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
     const bool ok = qvalid && d0 < D;
-    qreg[s] = ok ? ld16(qcol + (tok0 + qi) * ld + d0) : kZero4;
+    qreg[s] = ok ? fold_operand(ld16(q0 + (int64_t)qi * ld + d0), f) : kZero4;
     doreg[s] = ok ? ld16(dout + obase + d0) : kZero4;
     if (ok) {
       const f32x4 o0 = *reinterpret_cast<const f32x4*>(out32 + obase + d0);
@@ -475,8 +547,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     }
   }
   const float delta = dsum + __shfl_xor(dsum, 32);
-  // +inf makes p = exp2(s - lse) exactly 0 on lanes past S (their s is finite).
-  const float lse_q = qvalid ? lse[(int64_t)bh * S + qi] : INFINITY;
+  // -inf makes p = exp2(acc c - lse) exactly 0 on lanes past S (their acc is finite).
+  const float neg_lse = qvalid ? -lse[(int64_t)bh * S + qi] : -INFINITY;
   if (qvalid && g == 0) delta_ws[(int64_t)bh * S + qi] = delta;
 
   f32x16 dq[G::DB];
@@ -486,25 +558,28 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
 
   float* myring = ring[wave * 2 + g];
+  uint32_t voff[CPT];
+  tile_offsets<DP, K::NT>(voff, ld, D);
   u32x4 kst[CPT], vst[CPT];
   float bst[K::BPT];
   const int T = (S + kStep - 1) / kStep;
-  load_tile<DP, K::NT>(kst, kcol, ld, tok0, 0, S, D);
-  load_tile<DP, K::NT>(vst, vcol, ld, tok0, 0, S, D);
-  load_bias<NW>(bst, pdh, npd, 0 - i_wg - (K::ROWS - 1) + S - 1, 1);
+  const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
+  load_tile<DP, K::NT>(kst, voff, k0p, ld, 0, S, D);
+  load_tile<DP, K::NT>(vst, voff, v0p, ld, 0, S, D);
+  load_bias<NW>(bst, pdh, npd, wb0, 1, f.bmul);
 
   // Stage step t (stash the prefetched tile, prefetch step t+1, fold finished diagonals).
   auto stage = [&](int t) {
-    const int j0 = t * kStep;
+    const int j1 = (t + 1) * kStep;
     __syncthreads();
     stash_tile<DP, K::NT>(kst, Ks);
     stash_tile<DP, K::NT>(vst, Vs);
     stash_bias<NW>(bst, Bw);
     __syncthreads();
     if (t + 1 < T) {
-      load_tile<DP, K::NT>(kst, kcol, ld, tok0, j0 + kStep, S, D);
-      load_tile<DP, K::NT>(vst, vcol, ld, tok0, j0 + kStep, S, D);
-      load_bias<NW>(bst, pdh, npd, j0 + kStep - i_wg - (K::ROWS - 1) + S - 1, 1);
+      load_tile<DP, K::NT>(kst, voff, k0p, ld, j1, S, D);
+      load_tile<DP, K::NT>(vst, voff, v0p, ld, j1, S, D);
+      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, f.bmul);
     }
     // Diagonals r in [64(t-1), 64t) received their last contribution in
     // iteration t-1: fold the rings in order into the partial row.
@@ -517,13 +592,13 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   const int Tfull = S / kStep;
   for (int t = 0; t < Tfull; ++t) {
     stage(t);
-    dq_step<DP, NW, false>(Ks, Vs, Bw, myring, qreg, doreg, dq, lse_q, delta, t * kStep, S, ii, g,
-                           l32, c0, c);
+    dq_step<DP, NW, false>(Ks, Vs, Bw, myring, qreg, doreg, dq, neg_lse, delta, t * kStep, S, ii,
+                           g, l32, c0, c);
   }
   if (Tfull < T) {
     stage(Tfull);
-    dq_step<DP, NW, true>(Ks, Vs, Bw, myring, qreg, doreg, dq, lse_q, delta, Tfull * kStep, S, ii,
-                          g, l32, c0, c);
+    dq_step<DP, NW, true>(Ks, Vs, Bw, myring, qreg, doreg, dq, neg_lse, delta, Tfull * kStep, S,
+                          ii, g, l32, c0, c);
   }
 
   __syncthreads();
@@ -552,10 +627,10 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H,
-    int D, float c, float scale) {
+    int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int CPT = (G::NCH + K::NT - 1) / K::NT;
+  constexpr int CPT = Tile<DP, K::NT>::CPT;
   __shared__ __attribute__((aligned(16))) uint16_t Qs[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) uint16_t Os[kStep * G::RLD];
   __shared__ __attribute__((aligned(16))) float Lq[kStep];
@@ -570,15 +645,14 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   const bool kvalid = kj < S;
   const int64_t tok0 = (int64_t)b * S;
   const int64_t HD = (int64_t)H * D;
-  const uint16_t* qcol = qkv + (int64_t)h * D;
-  const uint16_t* kcol = qkv + HD + (int64_t)h * D;
-  const uint16_t* vcol = qkv + 2 * HD + (int64_t)h * D;
-  const uint16_t* ocol = dout + (int64_t)h * D;
+  const uint16_t* q0 = qkv + tok0 * ld + (int64_t)h * D;
+  const uint16_t* o0 = dout + tok0 * HD + (int64_t)h * D;  // row 0 of this (batch, head)'s dO
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
   const float* lse_bh = lse + (int64_t)bh * S;
   const float* dl_bh = delta_ws + (int64_t)bh * S;
   const int c0 = 16 * ((lane >> 4) & 1);
+  const float c = f.c;
 
   zero_pad_cols<DP, K::NT>(Qs);
   zero_pad_cols<DP, K::NT>(Os);
@@ -588,8 +662,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
     const bool ok = kvalid && d0 < D;
-    kreg[s] = ok ? ld16(kcol + (tok0 + kj) * ld + d0) : kZero4;
-    vreg[s] = ok ? ld16(vcol + (tok0 + kj) * ld + d0) : kZero4;
+    kreg[s] = ok ? fold_operand(ld16(q0 + HD + (int64_t)kj * ld + d0), f) : kZero4;
+    vreg[s] = ok ? ld16(q0 + 2 * HD + (int64_t)kj * ld + d0) : kZero4;
   }
 
   f32x16 dk[G::DB], dv[G::DB];
@@ -598,24 +672,29 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
+  uint32_t qoff[CPT], ooff[CPT];
+  tile_offsets<DP, K::NT>(qoff, ld, D);
+  tile_offsets<DP, K::NT>(ooff, HD, D);
   u32x4 qst[CPT], ost[CPT];
   float bst[K::BPT];
   float sst = 0.f;
   const int T = (S + kStep - 1) / kStep;
-  // Per-query statistics of the step: threads 0..63 lse, 64..127 delta. Rows past S get
-  // lse = +inf, which makes their p = exp2(s - lse) exactly 0 (s is finite there).
+  // Per-query statistics of the step: threads 0..63 -lse, 64..127 delta. Rows past S get
+  // -lse = -inf, which makes their p = exp2(acc c - lse) exactly 0 (acc is finite there).
   auto stats = [&](int i0) {
     const int q = i0 + (tid & 63);
-    if (tid < 128) sst = q < S ? (tid < 64 ? lse_bh[q] : dl_bh[q]) : (tid < 64 ? INFINITY : 0.f);
+    if (tid < 128) sst = q < S ? (tid < 64 ? -lse_bh[q] : dl_bh[q]) : (tid < 64 ? -INFINITY : 0.f);
   };
-  // Reversed window: entry x holds T[rb - x], rb the largest diagonal of the step.
-  load_tile<DP, K::NT>(qst, qcol, ld, tok0, 0, S, D);
-  load_tile<DP, K::NT>(ost, ocol, HD, tok0, 0, S, D);
-  load_bias<NW>(bst, pdh, npd, (j_wg + K::ROWS - 1) - 0 + S - 1, -1);
+  // Reversed window: entry x holds T[rb - x], rb = (j_wg + ROWS - 1) - i0 + S - 1 the largest
+  // diagonal of the step.
+  const int rb0 = (j_wg + K::ROWS - 1) + S - 1;
+  load_tile<DP, K::NT>(qst, qoff, q0, ld, 0, S, D);
+  load_tile<DP, K::NT>(ost, ooff, o0, HD, 0, S, D);
+  load_bias<NW>(bst, pdh, npd, rb0, -1, f.bmul);
   stats(0);
 
   for (int t = 0; t < T; ++t) {
-    const int i0 = t * kStep;
+    const int i1 = (t + 1) * kStep;
     __syncthreads();
     stash_tile<DP, K::NT>(qst, Qs);
     stash_tile<DP, K::NT>(ost, Os);
@@ -626,32 +705,30 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       Dq[tid - 64] = sst;
     __syncthreads();
     if (t + 1 < T) {
-      load_tile<DP, K::NT>(qst, qcol, ld, tok0, i0 + kStep, S, D);
-      load_tile<DP, K::NT>(ost, ocol, HD, tok0, i0 + kStep, S, D);
-      load_bias<NW>(bst, pdh, npd, (j_wg + K::ROWS - 1) - (i0 + kStep) + S - 1, -1);
-      stats(i0 + kStep);
+      load_tile<DP, K::NT>(qst, qoff, q0, ld, i1, S, D);
+      load_tile<DP, K::NT>(ost, ooff, o0, HD, i1, S, D);
+      load_bias<NW>(bst, pdh, npd, rb0 - i1, -1, f.bmul);
+      stats(i1);
     }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      f32x16 acc, accp;
+      f32x16 acc = read_bias16<NW>(Bw, (K::ROWS - 1) - kk + qb * 32 + 4 * g), accp;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = accp[r] = 0.f;
+      for (int r = 0; r < 16; ++r) accp[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < G::KS; ++s) {
         acc = mfma32x32x16(ld16(Qs + (qb * 32 + l32) * G::RLD + 16 * s + 8 * g), kreg[s], acc);
         accp = mfma32x32x16(ld16(Os + (qb * 32 + l32) * G::RLD + 16 * s + 8 * g), vreg[s], accp);
       }
-      float bias[16];
-      read_bias16<NW>(Bw, (K::ROWS - 1) - kk + qb * 32 + 4 * g, bias);
       float p[16], ds[16];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(Lq + qb * 32 + 8 * a + 4 * g);
+        const f32x4 nl4 = *reinterpret_cast<const f32x4*>(Lq + qb * 32 + 8 * a + 4 * g);
         const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dq + qb * 32 + 8 * a + 4 * g);
 #pragma unroll
         for (int b4 = 0; b4 < 4; ++b4) {
           const int r = 4 * a + b4;
-          const float pv = __builtin_amdgcn_exp2f(acc[r] * c + bias[r] - l4[b4]);
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], c, nl4[b4]));
           p[r] = pv;
           ds[r] = pv * (accp[r] - d4[b4]);
         }
@@ -722,14 +799,29 @@ constexpr int kFwdNW = 4;
 constexpr int kDqNW = 4;
 constexpr int kDkdvNW = 4;
 
+// Smallest nonzero |scale| * log2(e) the folded bias accepts: pd * log2(e) / c must
+// stay finite for any realistic table.
+constexpr float kMinScaleLog2 = 8.67361737988403547e-19f;  // 2^-60
+
 int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float scale) {
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return KRSI_ERR_BAD_SHAPE;
   if (D % 8 != 0 || D > 128) return KRSI_ERR_UNSUPPORTED;
   if ((int64_t)B * H > 65535 || S > (1 << 24)) return KRSI_ERR_BAD_SHAPE;
   if (ld < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
+  // Buffer resources of one (batch, head) slice hold S rows of ld bf16 in < 2^31 bytes.
+  if ((int64_t)S * ld * 2 >= ((int64_t)1 << 31)) return KRSI_ERR_UNSUPPORTED;
   if (ld % 8 != 0 || !aligned16(qkv)) return KRSI_ERR_MISALIGNED;
   if (!(scale == scale) || scale > 3.0e38f || scale < -3.0e38f) return KRSI_ERR_BAD_SCALE;
+  const float c = fabsf(scale * kLog2e);
+  if (c != 0.f && c < kMinScaleLog2) return KRSI_ERR_BAD_SCALE;
   return KRSI_OK;
+}
+
+Fold fold_scale(float scale) {
+  const float c = scale * kLog2e;
+  if (c == 0.f) return Fold{1.f, kLog2e, 0u, 0u};
+  const float a = fabsf(c);
+  return Fold{a, kLog2e / a, 0xffffffffu, c < 0.f ? 0x80008000u : 0u};
 }
 
 int padded_dim(int D) { return (D + 15) / 16 * 16; }
@@ -744,17 +836,17 @@ size_t ws_part_bytes(int B, int S, int H) {
 
 template <int DP>
 void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* out32, float* lse,
-                int B, int S, int H, int D, float c, hipStream_t st) {
+                int B, int S, int H, int D, Fold f, hipStream_t st) {
   using K = Blk<kFwdNW>;
   const dim3 grid((unsigned)ceil_div(S, K::ROWS), (unsigned)(B * H));
   hipLaunchKernelGGL((relpos_fwd_kernel<DP, kFwdNW>), grid, dim3(K::NT), 0, st,
-                     (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, c);
+                     (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
 }
 
 template <int DP>
 void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
                 const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S, int H,
-                int D, float c, float scale, hipStream_t st) {
+                int D, Fold f, float scale, hipStream_t st) {
   using KQ = Blk<kDqNW>;
   using KK = Blk<kDkdvNW>;
   float* delta = static_cast<float*>(ws);
@@ -762,11 +854,11 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   const int nqb = (int)ceil_div(S, KQ::ROWS);
   hipLaunchKernelGGL((relpos_bwd_dq_kernel<DP, kDqNW>), dim3((unsigned)nqb, (unsigned)(B * H)),
                      dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
-                     lse, delta, part, (uint16_t*)dqkv, ldd, S, H, D, c, scale);
+                     lse, delta, part, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
   hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DP, kDkdvNW>),
                      dim3((unsigned)ceil_div(S, KK::ROWS), (unsigned)(B * H)), dim3(KK::NT), 0, st,
                      (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse, (const float*)delta,
-                     (uint16_t*)dqkv, ldd, S, H, D, c, scale);
+                     (uint16_t*)dqkv, ldd, S, H, D, f, scale);
   const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
   hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S, H,
                      nqb, KQ::ROWS);
@@ -785,12 +877,12 @@ int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void*
   int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
   if (rc != KRSI_OK) return rc;
   if (!aligned16(out) || !aligned16(out32)) return KRSI_ERR_MISALIGNED;
-  const float c = scale * kLog2e;
+  const Fold f = fold_scale(scale);
   hipStream_t st = as_stream(stream);
   switch (padded_dim(D)) {
 #define KRSI_CASE(DPV_)                                                                \
   case DPV_:                                                                           \
-    launch_fwd<DPV_>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, c, st);             \
+    launch_fwd<DPV_>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, f, st);             \
     break;
     KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
     KRSI_CASE(112) KRSI_CASE(128)
@@ -822,13 +914,13 @@ int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, cons
   if (!workspace || workspace_bytes < krsi_relpos_bwd_workspace_bytes(B, S, H, D))
     return KRSI_ERR_WORKSPACE;
   if (!aligned16(workspace)) return KRSI_ERR_MISALIGNED;
-  const float c = scale * kLog2e;
+  const Fold f = fold_scale(scale);
   hipStream_t st = as_stream(stream);
   switch (padded_dim(D)) {
 #define KRSI_CASE(DPV_)                                                                      \
   case DPV_:                                                                                 \
     launch_bwd<DPV_>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace, B, S, \
-                     H, D, c, scale, st);                                                    \
+                     H, D, f, scale, st);                                                    \
     break;
     KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
     KRSI_CASE(112) KRSI_CASE(128)

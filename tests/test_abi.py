@@ -87,6 +87,8 @@ def test_validation_before_launch():
     assert fwd(ld=388) == E["ALIGN"]
     assert fwd(qkv=FAKE + 2) == E["ALIGN"]
     assert fwd(scale=float("inf")) == E["SCALE"]
+    assert fwd(scale=1e-25) == E["SCALE"]    # |scale| log2(e) below 2^-60 (folded bias overflow)
+    assert fwd(S=1 << 20, ld=1024) == E["UNSUP"]  # one (batch, head) slice >= 2^31 bytes
     assert fwd(pd=NULL) == E["NULL"]
     assert fwd(B=40000, H=2) == E["SHAPE"]   # B*H above the grid limit
     ws = lib.krsi_relpos_bwd_workspace_bytes(args["B"], args["S"], args["H"], args["D"])

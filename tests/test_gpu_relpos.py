@@ -88,6 +88,8 @@ CASES = [  # B, S, H, D, scale, qkv std, pd std
     (1, 96, 2, 96, 0.1, 1.0, 0.02),
     (1, 70, 1, 112, 0.1, 1.0, 0.02),
     (1, 257, 1, 8, 0.35, 1.0, 0.3),
+    (1, 96, 2, 64, -0.125, 1.0, 0.5),     # negative scale: sign folded into the bf16 operand
+    (1, 80, 2, 32, 0.0, 1.0, 1.0),        # scale 0: scores are the bias alone
 ]
 
 
