@@ -207,7 +207,9 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False) -> dict:
                            "ms": round(tb["ms_mean"], 4), "flops": fl_bwd,
                            "TFLOP/s": round(fl_bwd / tb["ms_mean"] / 1e9, 1)}},
            "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tfl / PEAK_BF16_TFLOPS, 4), "traffic": None}}
+                        "frac": round(tfl / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                        "scope": "one fwd+bwd step = relpos_fwd_kernel + relpos_bwd_dq_kernel + "
+                                 "relpos_bwd_dkdv_kernel + relpos_dpd_reduce, 14*B*H*L^2*D flops"}}
     if not args.no_cpu:
         import krsi_oracle as O
         nb = 2  # bounded sample: 2 of the B*H = 64 (batch, head) pairs, full L
@@ -221,6 +223,36 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False) -> dict:
                                "sample": f"reference eager torch SDPA-MATH fwd+bwd (bf16 in, fp32 math) on "
                                          f"{nb} of {B * H} (batch, head) pairs at L={S}, median of {reps} reps"}
     return res
+
+
+def _csrc_sha256() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "kernel-rsi_amd" / "csrc").glob("*")):
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+def attach_traffic(comps: dict) -> None:
+    """roofline.traffic = HBM bytes per step from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (profiles/traffic.json, scaled by a 2 GiB copy). Counters cannot be read inside this
+    process, so the figure is taken from those runs, and only while the kernel sources still hash
+    to what was profiled; otherwise it is null."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        rec = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return
+    fresh = rec.get("csrc_sha256") == _csrc_sha256()
+    for name, comp in comps.items():
+        t = rec.get("components", {}).get(name)
+        if t is None:
+            continue
+        comp["roofline"]["traffic"] = t["bytes_per_step"] if fresh else None
+        comp["roofline"]["traffic_unit"] = "bytes per step (HBM read + write)"
+        comp["roofline"]["traffic_source"] = t["summary"] if fresh else f"stale: {t['summary']} profiled other sources"
+        if fresh and comp.get("algorithmic_bytes"):
+            comp["roofline"]["traffic_vs_algorithmic"] = round(t["bytes_per_step"] / comp["algorithmic_bytes"], 3)
 
 
 def measured_copy_gbs() -> float:
@@ -268,6 +300,7 @@ def main() -> None:
         comps["rmsnorm"] = bench_rmsnorm(args)
     if "geglu" in only:
         comps["geglu"] = bench_geglu(args, "none")
+    attach_traffic(comps)
     head = comps.get("relpos_attention") or next(iter(comps.values()))
     line = {
         "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
