@@ -39,7 +39,7 @@
 //   * The Toeplitz bias of a (32*NW) x 64 tile is a window of consecutive table
 //     entries, staged once per step in 4 copies shifted by one entry, so every
 //     lane reads its 4 consecutive entries with one aligned 128-bit LDS read;
-//     the copy stride puts the 8 lanes of one read phase on distinct banks.
+//     the copy placement puts the 16 lanes of one read phase on distinct banks.
 //   * Online softmax keeps the exact running max per 64-key step (the step
 //     maximum gives p = 1, exact in bf16, as in the reference); the fp32
 //     accumulators are rescaled only when some lane's max moved. The row sum
@@ -54,6 +54,8 @@
 //     blocks in a fixed order. No [B, H, S, S] buffer exists.
 #include <math.h>
 
+#include <type_traits>
+
 #include "krsi_device.h"
 #include "krsi_internal.h"
 
@@ -61,14 +63,19 @@ namespace krsi {
 namespace {
 
 constexpr int kStep = 64;  // streamed positions per iteration
+
+// Compile-time buffer index and tail flag for the unrolled step loops.
+constexpr std::integral_constant<int, 0> kBuf0{};
+constexpr std::integral_constant<int, 1> kBuf1{};
+constexpr std::integral_constant<bool, false> kFull{};
+constexpr std::integral_constant<bool, true> kTail{};
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DP>
 struct Geo {
   static constexpr int KS = DP / 16;         // K steps of 16 over the head dim
   static constexpr int DB = (DP + 31) / 32;  // 32-wide head-dim blocks of head-dim outputs
-  static constexpr int DPV = DB * 32;
-  static constexpr int RLD = DPV + 8;        // row-major tile stride (bf16), padded
+  static constexpr int DPV = DB * 32;        // staged row length (bf16), zero padded past DP
   static constexpr int CPR = DP / 8;         // 16-byte chunks per staged row
   static constexpr int NCH = kStep * CPR;    // chunks per streamed tile
 };
@@ -77,8 +84,8 @@ template <int NW>
 struct Blk {
   static constexpr int ROWS = 32 * NW;             // queries or keys per workgroup
   static constexpr int NT = 64 * NW;               // threads per workgroup
-  static constexpr int WLD = ROWS + kStep + 8;     // bias copy stride, = 8 (mod 32) floats
-  static constexpr int WIN = WLD - 3;              // distinct window entries loaded
+  static constexpr int WIN = ROWS + kStep;         // distinct window entries loaded
+  static constexpr int WLD = ROWS + kStep + 16;    // bias copy stride, = 16 (mod 64) floats
   static constexpr int BPT = (WIN + NT - 1) / NT;  // window entries per thread
   static constexpr int RING = ROWS <= 128 ? 256 : 512;  // dpd ring (>= ROWS + 2 * kStep - 1)
 };
@@ -95,6 +102,7 @@ struct Fold {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr u32x4 kZero4 = {0u, 0u, 0u, 0u};
 
@@ -132,70 +140,128 @@ __device__ __forceinline__ float bload4(rsrc_t r, uint32_t voff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0));
 }
 
-// MFMA operand whose 8 K values are rows [k0, k0+4) and [k1, k1+4) of column
-// c0 + (lane % 16) of a row-major LDS tile (stride ld): two transposed reads,
-// in each of which lane s of a 16-lane group supplies row (k + s/4), columns
-// c0 + 4 (s % 4) .. +3. The caller passes c0 = block + 16 * ((lane / 16) % 2),
-// so lane l receives column block + l % 32.
-__device__ __forceinline__ u32x4 tr_operand(const uint16_t* tile, int ld, int k0, int k1, int c0) {
-  const int s = threadIdx.x & 15;
-  const int off = (s >> 2) * ld + c0 + 4 * (s & 3);
-  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + k0 * ld + off));
-  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + k1 * ld + off));
+// Staged tiles are row-major, DPV bf16 per row, with the 16-byte chunks of row r
+// permuted by chunk j -> j ^ swz(r). With 64 LDS banks of 4 bytes (16 quads of 16 bytes)
+// the permutation makes every access pattern of these kernels conflict-free:
+//   * 128-bit row reads (16 lanes per cycle = 16 consecutive rows, one chunk),
+//   * transposed 64-bit reads (32 lanes per cycle = 4 consecutive rows x 4 chunks),
+//   * 128-bit staging writes of whole rows (DP a multiple of 32).
+// swz only depends on bits 0-3 of r, so rows 16 apart share it.
+template <int DPV>
+__device__ __forceinline__ int swz(int r) {
+  constexpr int C = DPV / 8;
+  if constexpr (C == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else if constexpr (C == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (r >> 2) & 3;  // C = 4 or 12: permute within aligned groups of 4 chunks
+}
+template <int DPV>
+__device__ __forceinline__ int tile_off(int r, int j) { return r * DPV + 8 * (j ^ swz<DPV>(r)); }
+
+// Per-lane element offsets into a staged tile, fixed for the kernel's life.
+//   row[s]:    A/B operand of a product over the head dim: row l%32, columns 16s + 8(l/32) ..+7
+//              (add base * DPV for rows base + l%32, base a multiple of 16).
+//   tr[db][h]: transposed read for rows k + 8h + s/4, k = 16m + 4(l/32), s = l%16,
+//              columns 32db + 16((l/16)%2) + 4(s%4) ..+3 (add 16m * DPV).
+template <int DP>
+struct TileLane {
+  int row[Geo<DP>::KS];
+  int tr[Geo<DP>::DB][2];
+  __device__ __forceinline__ void init(int lane) {
+    constexpr int DPV = Geo<DP>::DPV;
+    const int l32 = lane & 31, g = lane >> 5, s = lane & 15;
+#pragma unroll
+    for (int k = 0; k < Geo<DP>::KS; ++k) row[k] = tile_off<DPV>(l32, 2 * k + g);
+#pragma unroll
+    for (int db = 0; db < Geo<DP>::DB; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 4 * g + 8 * h + (s >> 2);
+        const int j = 4 * db + 2 * ((lane >> 4) & 1) + ((s & 3) >> 1);
+        tr[db][h] = tile_off<DPV>(r, j) + 4 * (s & 1);
+      }
+  }
+};
+
+// MFMA operand whose 8 K values are rows [k, k+4) and [k+8, k+12) (k = 16m + 4(l/32))
+// of column 32db + l%32 of a staged tile: two ds_read_b64_tr_b16, in each of which lane
+// s of a 16-lane group supplies the address of row (k + s/4), columns 4(s%4)..+3 of its
+// 16-column block, and receives 4 consecutive rows of its own column.
+template <int DP>
+__device__ __forceinline__ u32x4 tr_operand(const uint16_t* tile, const TileLane<DP>& L, int m, int db) {
+  const uint16_t* t = tile + 16 * m * Geo<DP>::DPV;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + L.tr[db][0]));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + L.tr[db][1]));
   const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
   return u32x4{ua.x, ua.y, ub.x, ub.y};
 }
 
-// Streamed tiles. Chunk c = threadIdx.x + k * NT of a tile is row c / CPR, head-dim
-// columns d0 = 8 (c % CPR) .. +7. Its byte offset from the tile's first row is fixed
-// per thread; chunks past D (or past the tile) get kOob and read as zero.
+// 128-bit row read of the operand for head-dim step s: rows base + l%32.
+template <int DP>
+__device__ __forceinline__ u32x4 row_operand(const uint16_t* tile, const TileLane<DP>& L, int base, int s) {
+  return ld16(tile + base * Geo<DP>::DPV + L.row[s]);
+}
+
+// Lane l gets max / sum of x over lanes l % 32 and l % 32 + 32 (v_permlane32_swap_b32
+// exchanges the upper half of its first operand with the lower half of its second; the
+// nops cover the VALU-write -> permlane-read hazard).
+__device__ __forceinline__ void xhalf_pair(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float xhalf_max(float x) {
+  float a, b;
+  xhalf_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  float a, b;
+  xhalf_pair(x, a, b);
+  return a + b;
+}
+
+// Streamed tiles go straight from HBM into LDS (buffer_load_dwordx4 ... lds): lane l of
+// a wave writes the 16 bytes it loads to M0 + 16 l, so a wave fills 64 consecutive
+// 16-byte chunks of the staged tile. Group k of thread t fills LDS chunk p = k NT + t,
+// which is position p % C of staged row p / C (C = DPV / 8 chunks per row), so it loads
+// logical chunk (p % C) ^ swz(row) of that row. Chunks past D (the zero padding up to DPV)
+// get kOob and land as zeros, as do rows past S (the resource ends at row S - 1).
 template <int DP, int NT>
-struct Tile {
-  static constexpr int CPT = (Geo<DP>::NCH + NT - 1) / NT;
+struct Dma {
+  static constexpr int C = Geo<DP>::DPV / 8;
+  static constexpr int GPT = kStep * C / NT;  // chunks per thread per tile
+  static_assert(kStep * C % NT == 0, "tile chunks must split evenly over the workgroup");
 };
 
 template <int DP, int NT>
-__device__ __forceinline__ void tile_offsets(uint32_t* voff, int64_t ld, int D) {
-  using G = Geo<DP>;
+__device__ __forceinline__ void dma_offsets(uint32_t* voff, int64_t ld, int D) {
+  constexpr int C = Dma<DP, NT>::C;
 #pragma unroll
-  for (int k = 0; k < Tile<DP, NT>::CPT; ++k) {
-    const int c = threadIdx.x + k * NT;
-    const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
-    voff[k] = opaque((c < G::NCH && d0 < D) ? (uint32_t)(row * ld + d0) * 2u : kOob);
+  for (int k = 0; k < Dma<DP, NT>::GPT; ++k) {
+    const int p = k * NT + threadIdx.x;
+    const int row = p / C;
+    const int j = (p - row * C) ^ swz<Geo<DP>::DPV>(row);
+    voff[k] = opaque(8 * j < D ? (uint32_t)(row * ld + 8 * j) * 2u : kOob);
   }
 }
 
-// Rows p0..p0+63 of the [S, D] slice whose row 0 is `origin` (row stride ld): the
-// resource ends at the last byte of row S-1, so rows >= S read as zero.
+// Rows p0..p0+63 of the [S, D] slice whose row 0 is `origin` (row stride ld) into the
+// staged tile at `tile`, asynchronously (vmcnt): wait and barrier before reading it.
 template <int DP, int NT>
-__device__ __forceinline__ void load_tile(u32x4* regs, const uint32_t* voff, const uint16_t* origin,
-                                          int64_t ld, int p0, int S, int D) {
+__device__ __forceinline__ void dma_tile(uint16_t* tile, const uint32_t* voff, const uint16_t* origin,
+                                         int64_t ld, int p0, int S, int D) {
   const rsrc_t r = make_rsrc(origin + (int64_t)p0 * ld, (uint32_t)(((int64_t)(S - 1 - p0) * ld + D) * 2));
+  const int w = threadIdx.x >> 6;
 #pragma unroll
-  for (int k = 0; k < Tile<DP, NT>::CPT; ++k) regs[k] = bload16(r, voff[k]);
+  for (int k = 0; k < Dma<DP, NT>::GPT; ++k)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (k * NT + 64 * w) * 8), 16, voff[k], 0, 0, 0);
 }
 
-template <int DP, int NT>
-__device__ __forceinline__ void stash_tile(const u32x4* regs, uint16_t* tile) {
-  using G = Geo<DP>;
-#pragma unroll
-  for (int k = 0; k < Tile<DP, NT>::CPT; ++k) {
-    const int c = threadIdx.x + k * NT;
-    if (c < G::NCH) {
-      const int row = c / G::CPR, d0 = (c - row * G::CPR) * 8;
-      *reinterpret_cast<u32x4*>(tile + row * G::RLD + d0) = regs[k];
-    }
-  }
-}
-
-// Columns [DP, DPV) of a row-major tile are read by the transposed reads of the
-// last head-dim block and never staged: zero them once.
-template <int DP, int NT>
-__device__ __forceinline__ void zero_pad_cols(uint16_t* tile) {
-  using G = Geo<DP>;
-  constexpr int W = G::DPV - DP;
-  if (W > 0)
-    for (int e = threadIdx.x; e < kStep * W; e += NT) tile[(e / W) * G::RLD + DP + e % W] = 0;
+// Wait for this thread's outstanding loads (the tile DMA among them) and LDS operations,
+// then synchronise the workgroup.
+__device__ __forceinline__ void drain_and_sync() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
 }
 
 // Bias window entry x (0 <= x < WIN) holds T[wb + sgn * x] * bmul, zero outside
@@ -213,6 +279,12 @@ __device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd
   }
 }
 
+// Copy cc starts at cc * WLD, copy 0 at 4: with WLD = 16 (mod 64) the 16 lanes of one
+// 128-bit read phase (16 consecutive rows or columns, i.e. 16 consecutive x0) hit 16
+// distinct bank quads.
+template <int NW>
+__device__ __forceinline__ constexpr int copy_base(int cc) { return cc == 0 ? 4 : cc * Blk<NW>::WLD; }
+
 template <int NW>
 __device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
   using K = Blk<NW>;
@@ -221,7 +293,7 @@ __device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
     const int x = threadIdx.x + k * K::NT;
     if (x < K::WIN) {
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) bw[cc * K::WLD + x + cc] = regs[k];
+      for (int cc = 0; cc < 4; ++cc) bw[copy_base<NW>(cc) + x + cc] = regs[k];
     }
   }
 }
@@ -232,7 +304,7 @@ __device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
 template <int NW>
 __device__ __forceinline__ f32x16 read_bias16(const float* bw, int x0) {
   const int cc = (-x0) & 3;
-  const float* p = bw + cc * Blk<NW>::WLD + x0 + cc;
+  const float* p = bw + copy_base<NW>(cc) + x0 + cc;
   f32x16 out;
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
@@ -255,29 +327,52 @@ __device__ __forceinline__ float add_bf16_pair(uint32_t pair, float acc) {
 // O^T += V^T P^T. TAIL masks keys >= S (last step only).
 template <int DP, int NW, bool TAIL>
 __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
-                                         const u32x4* qreg, f32x16* oacc, float& m_run, float* l_run,
-                                         int j0, int S, int ii, int g, int l32, int c0, float c) {
+                                         const TileLane<DP>& L, const u32x4* qreg, f32x16* oacc,
+                                         float& m_run, float* l_run, int j0, int S, int ii, int g,
+                                         float c) {
   using G = Geo<DP>;
   using K = Blk<NW>;
+  // Up to DP = 96 all LDS operands of the score product are requested before its first
+  // MFMA and the transposed V operands before the softmax, so their latency overlaps the
+  // MFMAs and the exponentials (the register budget of larger head dims does not allow it).
+  constexpr bool kAhead = DP <= 96;
+  constexpr int KA = kAhead ? G::KS : 1;
+  constexpr int VA = kAhead ? 4 : 1;
   f32x16 sc[2];
+  u32x4 ka[2][KA];
+  u32x4 va[VA][G::DB];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     sc[kb] = read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii);
+    if constexpr (kAhead) {
 #pragma unroll
-    for (int s = 0; s < G::KS; ++s)
-      sc[kb] = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], sc[kb]);
-    if (TAIL) {
+      for (int s = 0; s < G::KS; ++s) ka[kb][s] = row_operand<DP>(Ks, L, kb * 32, s);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < G::KS; ++s)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      sc[kb] = mfma32x32x16(kAhead ? ka[kb][s] : row_operand<DP>(Ks, L, kb * 32, s), qreg[s], sc[kb]);
+  if constexpr (kAhead) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int db = 0; db < G::DB; ++db) va[m][db] = tr_operand<DP>(Vs, L, m, db);
+  }
+  if (TAIL) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) sc[kb][r] = -INFINITY;
-    }
   }
   float mx = fmaxf(sc[0][0], sc[1][0]);
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  mx = xhalf_max(mx) * c;
   // Exact running max, as the reference (relpos_attention.py:48-50): the step's largest
   // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
   // some lane's max moved.
@@ -304,10 +399,10 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
       const u32x4 pb = pack8(&p[8 * u]);
 #pragma unroll
       for (int w = 0; w < 4; ++w) l_run[w & 1] = add_bf16_pair(pb[w], l_run[w & 1]);
-      const int k0 = kb * 32 + 16 * u + 4 * g;
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
-        oacc[db] = mfma32x32x16(tr_operand(Vs, G::RLD, k0, k0 + 8, db * 32 + c0), pb, oacc[db]);
+        oacc[db] = mfma32x32x16(kAhead ? va[2 * kb + u][db] : tr_operand<DP>(Vs, L, 2 * kb + u, db), pb,
+                                oacc[db]);
     }
   }
 }
@@ -319,12 +414,15 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     int D, Fold f) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int CPT = Tile<DP, K::NT>::CPT;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
-  __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
+  constexpr int TILE = kStep * G::DPV;
+  constexpr int BWIN = 4 * K::WLD;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * TILE];
+  __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
+  TileLane<DP> L;
+  L.init(lane);
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
   const int i_wg = blockIdx.x * K::ROWS;
   const int ii = wave * 32 + l32;
@@ -337,10 +435,7 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
   const uint16_t* v0p = q0 + 2 * HD;
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
-  const int c0 = 16 * ((lane >> 4) & 1);
   const float c = f.c;
-
-  zero_pad_cols<DP, K::NT>(Vs);
 
   u32x4 qreg[G::KS];
 #pragma unroll
@@ -356,45 +451,50 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
   float m_run = -INFINITY, l_run[2] = {0.f, 0.f};
 
-  uint32_t voff[CPT];
-  tile_offsets<DP, K::NT>(voff, ld, D);
-  u32x4 kst[CPT], vst[CPT];
+  uint32_t voff[Dma<DP, K::NT>::GPT];
+  dma_offsets<DP, K::NT>(voff, ld, D);
   float bst[K::BPT];
   const int T = (S + kStep - 1) / kStep;
   // Window base of step t: entry x is table index wb + x, wb = j0 - i_wg - (ROWS-1) + S-1.
   const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
-  load_tile<DP, K::NT>(kst, voff, k0p, ld, 0, S, D);
-  load_tile<DP, K::NT>(vst, voff, v0p, ld, 0, S, D);
+  dma_tile<DP, K::NT>(Ks, voff, k0p, ld, 0, S, D);
+  dma_tile<DP, K::NT>(Vs, voff, v0p, ld, 0, S, D);
   load_bias<NW>(bst, pdh, npd, wb0, 1, f.bmul);
 
-  // Stage step t (stash the prefetched tile, then prefetch step t+1).
-  auto stage = [&](int t) {
-    const int j1 = (t + 1) * kStep;
-    __syncthreads();
-    stash_tile<DP, K::NT>(kst, Ks);
-    stash_tile<DP, K::NT>(vst, Vs);
-    stash_bias<NW>(bst, Bw);
-    __syncthreads();
+  // Step t computes from buffer t & 1, requested one step earlier. The one barrier per
+  // step publishes that buffer and retires every wave's reads of the other one (step t-1),
+  // which the requests for step t+1 then overwrite.
+  auto step = [&](int t, auto buf, auto tail) {
+    constexpr int B = decltype(buf)::value;
+    stash_bias<NW>(bst, Bw + B * BWIN);
+    drain_and_sync();
     if (t + 1 < T) {
-      load_tile<DP, K::NT>(kst, voff, k0p, ld, j1, S, D);
-      load_tile<DP, K::NT>(vst, voff, v0p, ld, j1, S, D);
+      const int j1 = (t + 1) * kStep;
+      dma_tile<DP, K::NT>(Ks + (1 - B) * TILE, voff, k0p, ld, j1, S, D);
+      dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
       load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, f.bmul);
     }
+    fwd_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, oacc,
+                                            m_run, l_run, t * kStep, S, ii, g, c);
   };
   // Full 64-key steps carry no key mask; a partial last step (S % 64 != 0) runs once after
-  // the loop, so the loop body holds a single copy of the step.
+  // the loop. The loop is unrolled by two so every buffer offset is a constant.
   const int Tfull = S / kStep;
-  for (int t = 0; t < Tfull; ++t) {
-    stage(t);
-    fwd_step<DP, NW, false>(Ks, Vs, Bw, qreg, oacc, m_run, l_run, t * kStep, S, ii, g, l32, c0, c);
+  int t = 0;
+  for (; t + 1 < Tfull; t += 2) {
+    step(t, kBuf0, kFull);
+    step(t + 1, kBuf1, kFull);
   }
-  if (Tfull < T) {
-    stage(Tfull);
-    fwd_step<DP, NW, true>(Ks, Vs, Bw, qreg, oacc, m_run, l_run, Tfull * kStep, S, ii, g, l32, c0, c);
+  if (t < Tfull) step(t++, kBuf0, kFull);
+  if (t < T) {
+    if (t & 1)
+      step(t, kBuf1, kTail);
+    else
+      step(t, kBuf0, kTail);
   }
 
   const float lh = l_run[0] + l_run[1];
-  const float l = lh + __shfl_xor(lh, 32);
+  const float l = xhalf_sum(lh);
   if (qvalid) {
     const int64_t obase = (tok0 + qi) * HD + (int64_t)h * D;
 #pragma unroll
@@ -444,9 +544,9 @@ __device__ __forceinline__ float ring_take(float (*ring)[Blk<NW>::RING + 32], in
 // >= S (last step only).
 template <int DP, int NW, bool TAIL>
 __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
-                                        float* myring, const u32x4* qreg, const u32x4* doreg,
-                                        f32x16* dq, float neg_lse, float delta, int j0, int S, int ii,
-                                        int g, int l32, int c0, float c) {
+                                        const TileLane<DP>& L, float* myring, const u32x4* qreg,
+                                        const u32x4* doreg, f32x16* dq, float neg_lse, float delta,
+                                        int j0, int S, int ii, int g, float c) {
   using G = Geo<DP>;
   using K = Blk<NW>;
 #pragma unroll
@@ -457,8 +557,8 @@ __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, 
     for (int r = 0; r < 16; ++r) accp[r] = 0.f;
 #pragma unroll
     for (int s = 0; s < G::KS; ++s) {
-      acc = mfma32x32x16(ld16(Ks + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), qreg[s], acc);
-      accp = mfma32x32x16(ld16(Vs + (kb * 32 + l32) * G::RLD + 16 * s + 8 * g), doreg[s], accp);
+      acc = mfma32x32x16(row_operand<DP>(Ks, L, kb * 32, s), qreg[s], acc);
+      accp = mfma32x32x16(row_operand<DP>(Vs, L, kb * 32, s), doreg[s], accp);
     }
     float ds[16];
 #pragma unroll
@@ -480,30 +580,32 @@ __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, 
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const u32x4 dsb = pack8(&ds[8 * u]);
-      const int k0 = kb * 32 + 16 * u + 4 * g;
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
-        dq[db] = mfma32x32x16(tr_operand(Ks, G::RLD, k0, k0 + 8, db * 32 + c0), dsb, dq[db]);
+        dq[db] = mfma32x32x16(tr_operand<DP>(Ks, L, 2 * kb + u, db), dsb, dq[db]);
     }
   }
 }
 
 template <int DP, int NW>
-__global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
+__global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ out32,
     const float* __restrict__ lse, float* __restrict__ delta_ws, float* __restrict__ part,
     uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H, int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int CPT = Tile<DP, K::NT>::CPT;
   constexpr int RING = K::RING;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kStep * G::RLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kStep * G::RLD];
-  __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
+  constexpr int TILE = kStep * G::DPV;
+  constexpr int BWIN = 4 * K::WLD;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * TILE];
+  __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
   __shared__ float ring[2 * NW][RING + 32];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  TileLane<DP> L;
+  L.init(lane);
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
   const int i_wg = blockIdx.x * K::ROWS;
   const int ii = wave * 32 + l32;
@@ -519,10 +621,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   const int RS = S + K::ROWS;         // partial row stride
   const int rlen = S + K::ROWS - 1;   // diagonals one query block touches
   float* prow = part + ((int64_t)bh * gridDim.x + blockIdx.x) * RS;
-  const int c0 = 16 * ((lane >> 4) & 1);
   const float c = f.c;
 
-  zero_pad_cols<DP, K::NT>(Ks);
   for (int e = tid; e < 2 * NW * (RING + 32); e += K::NT) (&ring[0][0])[e] = 0.f;
 
   // Register-resident operands and per-query statistics.
@@ -546,7 +646,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
       for (int e = 0; e < 4; ++e) dsum += df[4 + e] * o1[e];
     }
   }
-  const float delta = dsum + __shfl_xor(dsum, 32);
+  const float delta = xhalf_sum(dsum);
   // -inf makes p = exp2(acc c - lse) exactly 0 on lanes past S (their acc is finite).
   const float neg_lse = qvalid ? -lse[(int64_t)bh * S + qi] : -INFINITY;
   if (qvalid && g == 0) delta_ws[(int64_t)bh * S + qi] = delta;
@@ -558,47 +658,49 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
 
   float* myring = ring[wave * 2 + g];
-  uint32_t voff[CPT];
-  tile_offsets<DP, K::NT>(voff, ld, D);
-  u32x4 kst[CPT], vst[CPT];
+  uint32_t voff[Dma<DP, K::NT>::GPT];
+  dma_offsets<DP, K::NT>(voff, ld, D);
   float bst[K::BPT];
   const int T = (S + kStep - 1) / kStep;
   const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
-  load_tile<DP, K::NT>(kst, voff, k0p, ld, 0, S, D);
-  load_tile<DP, K::NT>(vst, voff, v0p, ld, 0, S, D);
+  dma_tile<DP, K::NT>(Ks, voff, k0p, ld, 0, S, D);
+  dma_tile<DP, K::NT>(Vs, voff, v0p, ld, 0, S, D);
   load_bias<NW>(bst, pdh, npd, wb0, 1, f.bmul);
 
-  // Stage step t (stash the prefetched tile, prefetch step t+1, fold finished diagonals).
-  auto stage = [&](int t) {
-    const int j1 = (t + 1) * kStep;
-    __syncthreads();
-    stash_tile<DP, K::NT>(kst, Ks);
-    stash_tile<DP, K::NT>(vst, Vs);
-    stash_bias<NW>(bst, Bw);
-    __syncthreads();
+  // Step t computes from buffer t & 1 (requested one step earlier); the barrier publishes
+  // it and retires every wave's reads of the other buffer and its ring updates of step t-1.
+  auto step = [&](int t, auto buf, auto tail) {
+    constexpr int B = decltype(buf)::value;
+    stash_bias<NW>(bst, Bw + B * BWIN);
+    drain_and_sync();
     if (t + 1 < T) {
-      load_tile<DP, K::NT>(kst, voff, k0p, ld, j1, S, D);
-      load_tile<DP, K::NT>(vst, voff, v0p, ld, j1, S, D);
+      const int j1 = (t + 1) * kStep;
+      dma_tile<DP, K::NT>(Ks + (1 - B) * TILE, voff, k0p, ld, j1, S, D);
+      dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
       load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, f.bmul);
     }
-    // Diagonals r in [64(t-1), 64t) received their last contribution in
-    // iteration t-1: fold the rings in order into the partial row.
+    // Diagonals r in [64(t-1), 64t) received their last contribution in step t-1 (step t
+    // touches [64t, 64t + 190]): fold the rings in order into the partial row.
     if (t > 0 && wave == 0) {
       const int r = (t - 1) * kStep + lane;
       prow[r] = ring_take<NW>(ring, r & (RING - 1), true);
     }
+    dq_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, myring,
+                                           qreg, doreg, dq, neg_lse, delta, t * kStep, S, ii, g, c);
   };
   // Full 64-key steps carry no key mask; a partial last step runs once after the loop.
   const int Tfull = S / kStep;
-  for (int t = 0; t < Tfull; ++t) {
-    stage(t);
-    dq_step<DP, NW, false>(Ks, Vs, Bw, myring, qreg, doreg, dq, neg_lse, delta, t * kStep, S, ii,
-                           g, l32, c0, c);
+  int t = 0;
+  for (; t + 1 < Tfull; t += 2) {
+    step(t, kBuf0, kFull);
+    step(t + 1, kBuf1, kFull);
   }
-  if (Tfull < T) {
-    stage(Tfull);
-    dq_step<DP, NW, true>(Ks, Vs, Bw, myring, qreg, doreg, dq, neg_lse, delta, Tfull * kStep, S,
-                          ii, g, l32, c0, c);
+  if (t < Tfull) step(t++, kBuf0, kFull);
+  if (t < T) {
+    if (t & 1)
+      step(t, kBuf1, kTail);
+    else
+      step(t, kBuf0, kTail);
   }
 
   __syncthreads();
@@ -630,14 +732,17 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
     int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int CPT = Tile<DP, K::NT>::CPT;
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[kStep * G::RLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Os[kStep * G::RLD];
-  __shared__ __attribute__((aligned(16))) float Lq[kStep];
-  __shared__ __attribute__((aligned(16))) float Dq[kStep];
-  __shared__ __attribute__((aligned(16))) float Bw[4 * K::WLD];
+  constexpr int TILE = kStep * G::DPV;
+  constexpr int BWIN = 4 * K::WLD;
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[2 * TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t Os[2 * TILE];
+  __shared__ __attribute__((aligned(16))) float Lq[2 * kStep];
+  __shared__ __attribute__((aligned(16))) float Dq[2 * kStep];
+  __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  TileLane<DP> L;
+  L.init(lane);
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
   const int j_wg = blockIdx.x * K::ROWS;
   const int kk = wave * 32 + l32;
@@ -651,11 +756,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   const float* pdh = pd + (int64_t)h * npd;
   const float* lse_bh = lse + (int64_t)bh * S;
   const float* dl_bh = delta_ws + (int64_t)bh * S;
-  const int c0 = 16 * ((lane >> 4) & 1);
   const float c = f.c;
-
-  zero_pad_cols<DP, K::NT>(Qs);
-  zero_pad_cols<DP, K::NT>(Os);
 
   u32x4 kreg[G::KS], vreg[G::KS];
 #pragma unroll
@@ -672,10 +773,9 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
-  uint32_t qoff[CPT], ooff[CPT];
-  tile_offsets<DP, K::NT>(qoff, ld, D);
-  tile_offsets<DP, K::NT>(ooff, HD, D);
-  u32x4 qst[CPT], ost[CPT];
+  uint32_t qoff[Dma<DP, K::NT>::GPT], ooff[Dma<DP, K::NT>::GPT];
+  dma_offsets<DP, K::NT>(qoff, ld, D);
+  dma_offsets<DP, K::NT>(ooff, HD, D);
   float bst[K::BPT];
   float sst = 0.f;
   const int T = (S + kStep - 1) / kStep;
@@ -688,43 +788,48 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   // Reversed window: entry x holds T[rb - x], rb = (j_wg + ROWS - 1) - i0 + S - 1 the largest
   // diagonal of the step.
   const int rb0 = (j_wg + K::ROWS - 1) + S - 1;
-  load_tile<DP, K::NT>(qst, qoff, q0, ld, 0, S, D);
-  load_tile<DP, K::NT>(ost, ooff, o0, HD, 0, S, D);
+  dma_tile<DP, K::NT>(Qs, qoff, q0, ld, 0, S, D);
+  dma_tile<DP, K::NT>(Os, ooff, o0, HD, 0, S, D);
   load_bias<NW>(bst, pdh, npd, rb0, -1, f.bmul);
   stats(0);
 
-  for (int t = 0; t < T; ++t) {
-    const int i1 = (t + 1) * kStep;
-    __syncthreads();
-    stash_tile<DP, K::NT>(qst, Qs);
-    stash_tile<DP, K::NT>(ost, Os);
-    stash_bias<NW>(bst, Bw);
+  // Step t computes from buffer t & 1 (requested one step earlier); the barrier publishes
+  // it and retires every wave's reads of the other buffer (step t-1).
+  auto step = [&](int t, auto buf) {
+    constexpr int B = decltype(buf)::value;
+    const uint16_t* Qb = Qs + B * TILE;
+    const uint16_t* Ob = Os + B * TILE;
+    const float* Bb = Bw + B * BWIN;
+    const float* Lb = Lq + B * kStep;
+    const float* Db = Dq + B * kStep;
+    stash_bias<NW>(bst, Bw + B * BWIN);
     if (tid < 64)
-      Lq[tid] = sst;
+      Lq[B * kStep + tid] = sst;
     else if (tid < 128)
-      Dq[tid - 64] = sst;
-    __syncthreads();
+      Dq[B * kStep + tid - 64] = sst;
+    drain_and_sync();
     if (t + 1 < T) {
-      load_tile<DP, K::NT>(qst, qoff, q0, ld, i1, S, D);
-      load_tile<DP, K::NT>(ost, ooff, o0, HD, i1, S, D);
+      const int i1 = (t + 1) * kStep;
+      dma_tile<DP, K::NT>(Qs + (1 - B) * TILE, qoff, q0, ld, i1, S, D);
+      dma_tile<DP, K::NT>(Os + (1 - B) * TILE, ooff, o0, HD, i1, S, D);
       load_bias<NW>(bst, pdh, npd, rb0 - i1, -1, f.bmul);
       stats(i1);
     }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      f32x16 acc = read_bias16<NW>(Bw, (K::ROWS - 1) - kk + qb * 32 + 4 * g), accp;
+      f32x16 acc = read_bias16<NW>(Bb, (K::ROWS - 1) - kk + qb * 32 + 4 * g), accp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) accp[r] = 0.f;
 #pragma unroll
       for (int s = 0; s < G::KS; ++s) {
-        acc = mfma32x32x16(ld16(Qs + (qb * 32 + l32) * G::RLD + 16 * s + 8 * g), kreg[s], acc);
-        accp = mfma32x32x16(ld16(Os + (qb * 32 + l32) * G::RLD + 16 * s + 8 * g), vreg[s], accp);
+        acc = mfma32x32x16(row_operand<DP>(Qb, L, qb * 32, s), kreg[s], acc);
+        accp = mfma32x32x16(row_operand<DP>(Ob, L, qb * 32, s), vreg[s], accp);
       }
       float p[16], ds[16];
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const f32x4 nl4 = *reinterpret_cast<const f32x4*>(Lq + qb * 32 + 8 * a + 4 * g);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(Dq + qb * 32 + 8 * a + 4 * g);
+        const f32x4 nl4 = *reinterpret_cast<const f32x4*>(Lb + qb * 32 + 8 * a + 4 * g);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(Db + qb * 32 + 8 * a + 4 * g);
 #pragma unroll
         for (int b4 = 0; b4 < 4; ++b4) {
           const int r = 4 * a + b4;
@@ -737,15 +842,22 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       for (int u = 0; u < 2; ++u) {
         const u32x4 pa = pack8(&p[8 * u]);
         const u32x4 dsa = pack8(&ds[8 * u]);
-        const int k0 = qb * 32 + 16 * u + 4 * g;
 #pragma unroll
         for (int db = 0; db < G::DB; ++db) {
-          dv[db] = mfma32x32x16(pa, tr_operand(Os, G::RLD, k0, k0 + 8, db * 32 + c0), dv[db]);
-          dk[db] = mfma32x32x16(dsa, tr_operand(Qs, G::RLD, k0, k0 + 8, db * 32 + c0), dk[db]);
+          dv[db] = mfma32x32x16(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
+          dk[db] = mfma32x32x16(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
         }
       }
     }
+  };
+  // Queries past S carry -lse = -inf (p = 0), so every step is unmasked; the loop is
+  // unrolled by two so every buffer offset is a constant.
+  int t = 0;
+  for (; t + 1 < T; t += 2) {
+    step(t, kBuf0);
+    step(t + 1, kBuf1);
   }
+  if (t < T) step(t, kBuf0);
 
   // D layout: lane = head dim d (n), register r = key 8(r/4) + 4g + r%4 of this wave.
 #pragma unroll
