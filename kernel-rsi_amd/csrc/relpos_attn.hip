@@ -229,8 +229,9 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 template <int DP, int NT>
 struct Dma {
   static constexpr int C = Geo<DP>::DPV / 8;
-  static constexpr int GPT = kStep * C / NT;  // chunks per thread per tile
-  static_assert(kStep * C % NT == 0, "tile chunks must split evenly over the workgroup");
+  static constexpr int NCHV = kStep * C;                // 16-byte chunks per staged tile
+  static constexpr int GPT = (NCHV + NT - 1) / NT;      // chunks per thread per tile
+  static_assert(NCHV % 64 == 0, "a wave fills whole 64-chunk runs");
 };
 
 template <int DP, int NT>
@@ -238,7 +239,7 @@ __device__ __forceinline__ void dma_offsets(uint32_t* voff, int64_t ld, int D) {
   constexpr int C = Dma<DP, NT>::C;
 #pragma unroll
   for (int k = 0; k < Dma<DP, NT>::GPT; ++k) {
-    const int p = k * NT + threadIdx.x;
+    const int p = min(k * NT + (int)threadIdx.x, Dma<DP, NT>::NCHV - 1);  // past the tile: unused
     const int row = p / C;
     const int j = (p - row * C) ^ swz<Geo<DP>::DPV>(row);
     voff[k] = opaque(8 * j < D ? (uint32_t)(row * ld + 8 * j) * 2u : kOob);
@@ -254,7 +255,8 @@ __device__ __forceinline__ void dma_tile(uint16_t* tile, const uint32_t* voff, c
   const int w = threadIdx.x >> 6;
 #pragma unroll
   for (int k = 0; k < Dma<DP, NT>::GPT; ++k)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (k * NT + 64 * w) * 8), 16, voff[k], 0, 0, 0);
+    if (Dma<DP, NT>::NCHV % NT == 0 || k * NT + 64 * w < Dma<DP, NT>::NCHV)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (k * NT + 64 * w) * 8), 16, voff[k], 0, 0, 0);
 }
 
 // Wait for this thread's outstanding loads (the tile DMA among them) and LDS operations,
@@ -313,6 +315,16 @@ __device__ __forceinline__ f32x16 read_bias16(const float* bw, int x0) {
     for (int b = 0; b < 4; ++b) out[4 * a + b] = v[b];
   }
   return out;
+}
+
+// Tile of a 1-D grid of N = (blocks per head) x (B*H) workgroups. Workgroups are handed
+// to the 8 XCDs round-robin by linear id and every XCD has its own L2, so XCD x gets the
+// contiguous tile range [x N/8, (x+1) N/8) in order: the blocks of one (batch, head) run
+// on one XCD at about the same time and share its streamed K/V (or Q/dO) tiles in L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_tile(int w, int N) {
+  const int x = w % kXcds, k = w / kXcds, q = N / kXcds, r = N % kXcds;
+  return x * q + min(x, r) + k;
 }
 
 // Row sum of bf16 p values: two per v_dot2c_f32_bf16 against (1, 1).
@@ -407,6 +419,34 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
   }
 }
 
+// O = acc / l stored as fp32 and bf16 (head-dim columns 32db + 8a + 4g ..+3 of this lane's
+// query), lse = m + log2 l.
+template <int DP>
+__device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const float* l_run,
+                                          bool qvalid, int g, int64_t obase, int D,
+                                          uint16_t* __restrict__ out, float* __restrict__ out32,
+                                          float* __restrict__ lse_q) {
+  const float l = xhalf_sum(l_run[0] + l_run[1]);
+  if (!qvalid) return;
+#pragma unroll
+  for (int db = 0; db < Geo<DP>::DB; ++db)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int d0 = db * 32 + 8 * a + 4 * g;
+      if (d0 < D) {
+        f32x4 o;
+#pragma unroll
+        for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
+        *reinterpret_cast<f32x4*>(out32 + obase + d0) = o;
+        uint2 ob;
+        ob.x = pack_bf16x2(o[0], o[1]);
+        ob.y = pack_bf16x2(o[2], o[3]);
+        *reinterpret_cast<uint2*>(out + obase + d0) = ob;
+      }
+    }
+  if (g == 0) *lse_q = m_run + log2f(l);
+}
+
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
@@ -423,8 +463,11 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
   L.init(lane);
-  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int i_wg = blockIdx.x * K::ROWS;
+  const int nqb = (S + K::ROWS - 1) / K::ROWS;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int bh = tile / nqb, b = bh / H, h = bh - b * H;
+  const int qb = tile - bh * nqb;
+  const int i_wg = qb * K::ROWS;
   const int ii = wave * 32 + l32;
   const int qi = i_wg + ii;
   const bool qvalid = qi < S;
@@ -493,28 +536,8 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
       step(t, kBuf0, kTail);
   }
 
-  const float lh = l_run[0] + l_run[1];
-  const float l = xhalf_sum(lh);
-  if (qvalid) {
-    const int64_t obase = (tok0 + qi) * HD + (int64_t)h * D;
-#pragma unroll
-    for (int db = 0; db < G::DB; ++db)
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d0 = db * 32 + 8 * a + 4 * g;
-        if (d0 < D) {
-          f32x4 o;
-#pragma unroll
-          for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
-          *reinterpret_cast<f32x4*>(out32 + obase + d0) = o;
-          uint2 ob;
-          ob.x = pack_bf16x2(o[0], o[1]);
-          ob.y = pack_bf16x2(o[2], o[3]);
-          *reinterpret_cast<uint2*>(out + obase + d0) = ob;
-        }
-      }
-    if (g == 0) lse[(int64_t)bh * S + qi] = m_run + log2f(l);
-  }
+  fwd_store<DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
+                lse + (int64_t)bh * S + qi);
 }
 
 // ------------------------------------------------ backward: delta, dQ and dpd
@@ -606,8 +629,11 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
   L.init(lane);
-  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int i_wg = blockIdx.x * K::ROWS;
+  const int nqb = (S + K::ROWS - 1) / K::ROWS;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int bh = tile / nqb, b = bh / H, h = bh - b * H;
+  const int qb = tile - bh * nqb;
+  const int i_wg = qb * K::ROWS;
   const int ii = wave * 32 + l32;
   const int qi = i_wg + ii;
   const bool qvalid = qi < S;
@@ -620,7 +646,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   const float* pdh = pd + (int64_t)h * npd;
   const int RS = S + K::ROWS;         // partial row stride
   const int rlen = S + K::ROWS - 1;   // diagonals one query block touches
-  float* prow = part + ((int64_t)bh * gridDim.x + blockIdx.x) * RS;
+  float* prow = part + ((int64_t)bh * nqb + qb) * RS;
   const float c = f.c;
 
   for (int e = tid; e < 2 * NW * (RING + 32); e += K::NT) (&ring[0][0])[e] = 0.f;
@@ -743,8 +769,10 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
   L.init(lane);
-  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
-  const int j_wg = blockIdx.x * K::ROWS;
+  const int nkb = (S + K::ROWS - 1) / K::ROWS;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int bh = tile / nkb, b = bh / H, h = bh - b * H;
+  const int j_wg = (tile - bh * nkb) * K::ROWS;
   const int kk = wave * 32 + l32;
   const int kj = j_wg + kk;
   const bool kvalid = kj < S;
@@ -950,7 +978,7 @@ template <int DP>
 void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* out32, float* lse,
                 int B, int S, int H, int D, Fold f, hipStream_t st) {
   using K = Blk<kFwdNW>;
-  const dim3 grid((unsigned)ceil_div(S, K::ROWS), (unsigned)(B * H));
+  const dim3 grid((unsigned)(ceil_div(S, K::ROWS) * B * H));
   hipLaunchKernelGGL((relpos_fwd_kernel<DP, kFwdNW>), grid, dim3(K::NT), 0, st,
                      (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
 }
@@ -964,11 +992,11 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   float* delta = static_cast<float*>(ws);
   float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_delta_bytes(B, S, H));
   const int nqb = (int)ceil_div(S, KQ::ROWS);
-  hipLaunchKernelGGL((relpos_bwd_dq_kernel<DP, kDqNW>), dim3((unsigned)nqb, (unsigned)(B * H)),
+  hipLaunchKernelGGL((relpos_bwd_dq_kernel<DP, kDqNW>), dim3((unsigned)(nqb * B * H)),
                      dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
                      lse, delta, part, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
   hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DP, kDkdvNW>),
-                     dim3((unsigned)ceil_div(S, KK::ROWS), (unsigned)(B * H)), dim3(KK::NT), 0, st,
+                     dim3((unsigned)(ceil_div(S, KK::ROWS) * B * H)), dim3(KK::NT), 0, st,
                      (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse, (const float*)delta,
                      (uint16_t*)dqkv, ldd, S, H, D, f, scale);
   const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
