@@ -246,17 +246,27 @@ __device__ __forceinline__ void dma_offsets(uint32_t* voff, int64_t ld, int D) {
   }
 }
 
+// One buffer_load_dwordx4 ... lds. It is issued from asm on purpose: the compiler treats
+// the builtin form as an LDS write of unknown extent and waits for it before every later
+// LDS read, which would complete each step's prefetch before that step's own compute.
+// Invisible to the compiler, the request stays in flight until the kernel's explicit
+// wait (drain_and_sync) at the top of the step that reads it; the compiler's own vmcnt
+// waits only ever over-wait because of it.
+__device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t m0) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(m0) : "memory");
+}
+
 // Rows p0..p0+63 of the [S, D] slice whose row 0 is `origin` (row stride ld) into the
 // staged tile at `tile`, asynchronously (vmcnt): wait and barrier before reading it.
 template <int DP, int NT>
 __device__ __forceinline__ void dma_tile(uint16_t* tile, const uint32_t* voff, const uint16_t* origin,
                                          int64_t ld, int p0, int S, int D) {
   const rsrc_t r = make_rsrc(origin + (int64_t)p0 * ld, (uint32_t)(((int64_t)(S - 1 - p0) * ld + D) * 2));
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
   for (int k = 0; k < Dma<DP, NT>::GPT; ++k)
     if (Dma<DP, NT>::NCHV % NT == 0 || k * NT + 64 * w < Dma<DP, NT>::NCHV)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (k * NT + 64 * w) * 8), 16, voff[k], 0, 0, 0);
+      dma16(r, voff[k], (uint32_t)(uintptr_t)(lds_void*)(tile + (k * NT + 64 * w) * 8));
 }
 
 // Wait for this thread's outstanding loads (the tile DMA among them) and LDS operations,
@@ -268,16 +278,17 @@ __device__ __forceinline__ void drain_and_sync() {
 
 // Bias window entry x (0 <= x < WIN) holds T[wb + sgn * x] * bmul, zero outside
 // [0, 2S - 1) (out-of-range offsets, negative ones included, fall past the
-// resource); it is stored at position x + cc of copy cc.
+// resource); it is stored at position x + cc of copy cc. The raw entries are loaded
+// one step ahead and scaled only when stashed, so nothing waits on the load (or on
+// the tile DMA issued next to it) before the step that consumes it.
 template <int NW>
-__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn,
-                                          float bmul) {
+__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn) {
   using K = Blk<NW>;
   const rsrc_t r = make_rsrc(pdh, (uint32_t)npd * 4u);
 #pragma unroll
   for (int k = 0; k < K::BPT; ++k) {
     const int x = threadIdx.x + k * K::NT;
-    regs[k] = x < K::WIN ? bload4(r, opaque((uint32_t)(wb + sgn * x) * 4u)) * bmul : 0.f;
+    regs[k] = bload4(r, opaque(x < K::WIN ? (uint32_t)(wb + sgn * x) * 4u : kOob));
   }
 }
 
@@ -288,14 +299,15 @@ template <int NW>
 __device__ __forceinline__ constexpr int copy_base(int cc) { return cc == 0 ? 4 : cc * Blk<NW>::WLD; }
 
 template <int NW>
-__device__ __forceinline__ void stash_bias(const float* regs, float* bw) {
+__device__ __forceinline__ void stash_bias(const float* regs, float* bw, float bmul) {
   using K = Blk<NW>;
 #pragma unroll
   for (int k = 0; k < K::BPT; ++k) {
     const int x = threadIdx.x + k * K::NT;
     if (x < K::WIN) {
+      const float v = regs[k] * bmul;
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) bw[copy_base<NW>(cc) + x + cc] = regs[k];
+      for (int cc = 0; cc < 4; ++cc) bw[copy_base<NW>(cc) + x + cc] = v;
     }
   }
 }
@@ -502,20 +514,20 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
   const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
   dma_tile<DP, K::NT>(Ks, voff, k0p, ld, 0, S, D);
   dma_tile<DP, K::NT>(Vs, voff, v0p, ld, 0, S, D);
-  load_bias<NW>(bst, pdh, npd, wb0, 1, f.bmul);
+  load_bias<NW>(bst, pdh, npd, wb0, 1);
 
   // Step t computes from buffer t & 1, requested one step earlier. The one barrier per
   // step publishes that buffer and retires every wave's reads of the other one (step t-1),
   // which the requests for step t+1 then overwrite.
   auto step = [&](int t, auto buf, auto tail) {
     constexpr int B = decltype(buf)::value;
-    stash_bias<NW>(bst, Bw + B * BWIN);
+    stash_bias<NW>(bst, Bw + B * BWIN, f.bmul);
     drain_and_sync();
     if (t + 1 < T) {
       const int j1 = (t + 1) * kStep;
       dma_tile<DP, K::NT>(Ks + (1 - B) * TILE, voff, k0p, ld, j1, S, D);
       dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
-      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, f.bmul);
+      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1);
     }
     fwd_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, oacc,
                                             m_run, l_run, t * kStep, S, ii, g, c);
@@ -691,19 +703,19 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
   dma_tile<DP, K::NT>(Ks, voff, k0p, ld, 0, S, D);
   dma_tile<DP, K::NT>(Vs, voff, v0p, ld, 0, S, D);
-  load_bias<NW>(bst, pdh, npd, wb0, 1, f.bmul);
+  load_bias<NW>(bst, pdh, npd, wb0, 1);
 
   // Step t computes from buffer t & 1 (requested one step earlier); the barrier publishes
   // it and retires every wave's reads of the other buffer and its ring updates of step t-1.
   auto step = [&](int t, auto buf, auto tail) {
     constexpr int B = decltype(buf)::value;
-    stash_bias<NW>(bst, Bw + B * BWIN);
+    stash_bias<NW>(bst, Bw + B * BWIN, f.bmul);
     drain_and_sync();
     if (t + 1 < T) {
       const int j1 = (t + 1) * kStep;
       dma_tile<DP, K::NT>(Ks + (1 - B) * TILE, voff, k0p, ld, j1, S, D);
       dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
-      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, f.bmul);
+      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1);
     }
     // Diagonals r in [64(t-1), 64t) received their last contribution in step t-1 (step t
     // touches [64t, 64t + 190]): fold the rings in order into the partial row.
@@ -807,18 +819,19 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   float bst[K::BPT];
   float sst = 0.f;
   const int T = (S + kStep - 1) / kStep;
-  // Per-query statistics of the step: threads 0..63 -lse, 64..127 delta. Rows past S get
-  // -lse = -inf, which makes their p = exp2(acc c - lse) exactly 0 (acc is finite there).
+  // Per-query statistics of the step, loaded one step ahead: wave 0 lse, wave 1 delta
+  // (zero past S through the buffer range check). Stashed as -lse, with -inf past S, which
+  // makes those rows' p = exp2(acc c - lse) exactly 0 (acc is finite there).
+  const rsrc_t rstat = make_rsrc(wave == 0 ? lse_bh : dl_bh, (uint32_t)S * 4u);
   auto stats = [&](int i0) {
-    const int q = i0 + (tid & 63);
-    if (tid < 128) sst = q < S ? (tid < 64 ? -lse_bh[q] : dl_bh[q]) : (tid < 64 ? -INFINITY : 0.f);
+    if (wave < 2) sst = bload4(rstat, opaque((uint32_t)(i0 + lane) * 4u));
   };
   // Reversed window: entry x holds T[rb - x], rb = (j_wg + ROWS - 1) - i0 + S - 1 the largest
   // diagonal of the step.
   const int rb0 = (j_wg + K::ROWS - 1) + S - 1;
   dma_tile<DP, K::NT>(Qs, qoff, q0, ld, 0, S, D);
   dma_tile<DP, K::NT>(Os, ooff, o0, HD, 0, S, D);
-  load_bias<NW>(bst, pdh, npd, rb0, -1, f.bmul);
+  load_bias<NW>(bst, pdh, npd, rb0, -1);
   stats(0);
 
   // Step t computes from buffer t & 1 (requested one step earlier); the barrier publishes
@@ -830,17 +843,17 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
     const float* Bb = Bw + B * BWIN;
     const float* Lb = Lq + B * kStep;
     const float* Db = Dq + B * kStep;
-    stash_bias<NW>(bst, Bw + B * BWIN);
-    if (tid < 64)
-      Lq[B * kStep + tid] = sst;
-    else if (tid < 128)
-      Dq[B * kStep + tid - 64] = sst;
+    stash_bias<NW>(bst, Bw + B * BWIN, f.bmul);
+    if (wave == 0)
+      Lq[B * kStep + lane] = t * kStep + lane < S ? -sst : -INFINITY;
+    else if (wave == 1)
+      Dq[B * kStep + lane] = sst;
     drain_and_sync();
     if (t + 1 < T) {
       const int i1 = (t + 1) * kStep;
       dma_tile<DP, K::NT>(Qs + (1 - B) * TILE, qoff, q0, ld, i1, S, D);
       dma_tile<DP, K::NT>(Os + (1 - B) * TILE, ooff, o0, HD, i1, S, D);
-      load_bias<NW>(bst, pdh, npd, rb0 - i1, -1, f.bmul);
+      load_bias<NW>(bst, pdh, npd, rb0 - i1, -1);
       stats(i1);
     }
 #pragma unroll
