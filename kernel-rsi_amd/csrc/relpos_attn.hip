@@ -356,33 +356,12 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
                                          float c) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  // Up to DP = 96 all LDS operands of the score product are requested before its first
-  // MFMA and the transposed V operands before the softmax, so their latency overlaps the
-  // MFMAs and the exponentials (the register budget of larger head dims does not allow it).
-  constexpr bool kAhead = DP <= 96;
-  constexpr int KA = kAhead ? G::KS : 1;
-  constexpr int VA = kAhead ? 4 : 1;
   f32x16 sc[2];
-  u32x4 ka[2][KA];
-  u32x4 va[VA][G::DB];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     sc[kb] = read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii);
-    if constexpr (kAhead) {
 #pragma unroll
-      for (int s = 0; s < G::KS; ++s) ka[kb][s] = row_operand<DP>(Ks, L, kb * 32, s);
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < G::KS; ++s)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-      sc[kb] = mfma32x32x16(kAhead ? ka[kb][s] : row_operand<DP>(Ks, L, kb * 32, s), qreg[s], sc[kb]);
-  if constexpr (kAhead) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int db = 0; db < G::DB; ++db) va[m][db] = tr_operand<DP>(Vs, L, m, db);
+    for (int s = 0; s < G::KS; ++s) sc[kb] = mfma32x32x16(row_operand<DP>(Ks, L, kb * 32, s), qreg[s], sc[kb]);
   }
   if (TAIL) {
 #pragma unroll
@@ -425,8 +404,7 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
       for (int w = 0; w < 4; ++w) l_run[w & 1] = add_bf16_pair(pb[w], l_run[w & 1]);
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
-        oacc[db] = mfma32x32x16(kAhead ? va[2 * kb + u][db] : tr_operand<DP>(Vs, L, 2 * kb + u, db), pb,
-                                oacc[db]);
+        oacc[db] = mfma32x32x16(tr_operand<DP>(Vs, L, 2 * kb + u, db), pb, oacc[db]);
     }
   }
 }
