@@ -44,14 +44,15 @@
 //     maximum gives p = 1, exact in bf16, as in the reference); the fp32
 //     accumulators are rescaled only when some lane's max moved. The row sum
 //     adds the bf16 p the PV product uses (v_dot2c_f32_bf16, two per op).
-//   * dpd is reduced along the diagonals j - i inside the dQ kernel: each
-//     (wave, half-wave) adds its fp32 ds into a private LDS ring indexed by
-//     diagonal. Within one register the 32 lanes of a half-wave hit distinct
-//     slots and a wave's LDS operations complete in order, so a plain
-//     read-modify-write is exact and deterministic. Diagonals that can get no
-//     further contribution are folded in a fixed order into one partial row per
-//     query block; a last kernel sums the partial rows over batch and query
-//     blocks in a fixed order. No [B, H, S, S] buffer exists.
+//   * dpd is reduced along the diagonals j - i inside the dK/dV kernel: each
+//     (wave, half-wave) adds its fp32 ds into private LDS rings indexed by
+//     diagonal, two diagonals per 64-bit read-modify-write. Within one
+//     instruction the lanes of a ring hit distinct slots and a wave's LDS
+//     operations complete in order, so the plain read-modify-write is exact and
+//     deterministic. Diagonals that can get no further contribution are folded
+//     in a fixed order into one partial row per key block; a last kernel sums
+//     the partial rows over batch and key blocks in a fixed order. No
+//     [B, H, S, S] buffer exists.
 #include <math.h>
 
 #include <type_traits>
@@ -87,7 +88,6 @@ struct Blk {
   static constexpr int WIN = ROWS + kStep;         // distinct window entries loaded
   static constexpr int WLD = ROWS + kStep + 16;    // bias copy stride, = 16 (mod 64) floats
   static constexpr int BPT = (WIN + NT - 1) / NT;  // window entries per thread
-  static constexpr int RING = ROWS <= 128 ? 256 : 512;  // dpd ring (>= ROWS + 2 * kStep - 1)
 };
 
 // Scale folding: scores are acc * c with acc = q'.k + pd * bmul, q' = (q & qand) ^ qxor
@@ -531,35 +531,14 @@ __global__ __launch_bounds__(64 * NW, 2) void relpos_fwd_kernel(
 }
 
 // ------------------------------------------------ backward: delta, dQ and dpd
-// Diagonal ring of the dQ kernel: RING slots indexed by diagonal mod RING, plus a
-// 32-slot overflow zone that aliases slots 0..31, so the 16 updates of one D tile
-// (diagonals base + 8a + b, a, b < 4) use one base register and immediate offsets.
-// Folding a diagonal reads (and clears) both of its slots.
-template <int NW>
-__device__ __forceinline__ float ring_take(float (*ring)[Blk<NW>::RING + 32], int slot, bool clear) {
-  constexpr int RING = Blk<NW>::RING;
-  float v = 0.f;
-#pragma unroll
-  for (int k = 0; k < 2 * NW; ++k) {
-    v += ring[k][slot];
-    if (clear) ring[k][slot] = 0.f;
-    if (slot < 32) {
-      v += ring[k][slot + RING];
-      if (clear) ring[k][slot + RING] = 0.f;
-    }
-  }
-  return v;
-}
-
 // One 64-key step of the dQ kernel for this lane's query: p = exp2(acc c - lse),
-// ds = p (dp - delta), ds into the diagonal ring, dQ^T += K^T dS^T. Invalid
-// query lanes carry lse = +inf, so their p is 0 without a mask; TAIL masks keys
-// >= S (last step only).
+// ds = p (dp - delta), dQ^T += K^T dS^T. Invalid query lanes carry lse = +inf, so
+// their p is 0 without a mask; TAIL masks keys >= S (last step only).
 template <int DP, int NW, bool TAIL>
 __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
-                                        const TileLane<DP>& L, float* myring, const u32x4* qreg,
-                                        const u32x4* doreg, f32x16* dq, float neg_lse, float delta,
-                                        int j0, int S, int ii, int g, float c) {
+                                        const TileLane<DP>& L, const u32x4* qreg, const u32x4* doreg,
+                                        f32x16* dq, float neg_lse, float delta, int j0, int S, int ii,
+                                        int g, float c) {
   using G = Geo<DP>;
   using K = Blk<NW>;
 #pragma unroll
@@ -580,16 +559,6 @@ __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, 
       if (TAIL && j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= S) p = 0.f;
       ds[r] = p * (accp[r] - delta);
     }
-    // Diagonal of D-register r: j - i + ROWS - 1 - i_wg = j0 + x0 + 8a + b. Within one
-    // register the 32 lanes of a half hit 32 distinct diagonals of their own ring, and LDS
-    // operations of a wave complete in order, so a plain read-modify-write per register is
-    // exact (LDS float atomics cost ~30x more here). Lanes ii and ii+1 reach the same
-    // diagonal through neighbouring registers, so the read-modify-writes must stay in
-    // register order: the accesses are volatile, which forbids batching the reads ahead of
-    // the writes (the compiler only sees that one lane's 16 slots are distinct).
-    volatile lds_f32* rp = (volatile lds_f32*)myring + ((j0 + x0) & (K::RING - 1));
-#pragma unroll
-    for (int r = 0; r < 16; ++r) rp[8 * (r >> 2) + (r & 3)] = rp[8 * (r >> 2) + (r & 3)] + ds[r];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const u32x4 dsb = pack8(&ds[8 * u]);
@@ -604,17 +573,15 @@ template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ out32,
-    const float* __restrict__ lse, float* __restrict__ delta_ws, float* __restrict__ part,
-    uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H, int D, Fold f, float scale) {
+    const float* __restrict__ lse, float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv,
+    int64_t ldd, int S, int H, int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
-  constexpr int RING = K::RING;
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * TILE];
   __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
-  __shared__ float ring[2 * NW][RING + 32];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
@@ -634,12 +601,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   const uint16_t* v0p = q0 + 2 * HD;
   const int npd = 2 * S - 1;
   const float* pdh = pd + (int64_t)h * npd;
-  const int RS = S + K::ROWS;         // partial row stride
-  const int rlen = S + K::ROWS - 1;   // diagonals one query block touches
-  float* prow = part + ((int64_t)bh * nqb + qb) * RS;
   const float c = f.c;
 
-  for (int e = tid; e < 2 * NW * (RING + 32); e += K::NT) (&ring[0][0])[e] = 0.f;
 
   // Register-resident operands and per-query statistics.
   u32x4 qreg[G::KS], doreg[G::KS];
@@ -673,7 +636,6 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
 #pragma unroll
     for (int r = 0; r < 16; ++r) dq[db][r] = 0.f;
 
-  float* myring = ring[wave * 2 + g];
   uint32_t voff[Dma<DP, K::NT>::GPT];
   dma_offsets<DP, K::NT>(voff, ld, D);
   float bst[K::BPT];
@@ -684,7 +646,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   load_bias<NW>(bst, pdh, npd, wb0, 1);
 
   // Step t computes from buffer t & 1 (requested one step earlier); the barrier publishes
-  // it and retires every wave's reads of the other buffer and its ring updates of step t-1.
+  // it and retires every wave's reads of the other buffer.
   auto step = [&](int t, auto buf, auto tail) {
     constexpr int B = decltype(buf)::value;
     stash_bias<NW>(bst, Bw + B * BWIN, f.bmul);
@@ -695,14 +657,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
       dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
       load_bias<NW>(bst, pdh, npd, wb0 + j1, 1);
     }
-    // Diagonals r in [64(t-1), 64t) received their last contribution in step t-1 (step t
-    // touches [64t, 64t + 190]): fold the rings in order into the partial row.
-    if (t > 0 && wave == 0) {
-      const int r = (t - 1) * kStep + lane;
-      prow[r] = ring_take<NW>(ring, r & (RING - 1), true);
-    }
-    dq_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, myring,
-                                           qreg, doreg, dq, neg_lse, delta, t * kStep, S, ii, g, c);
+    dq_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, doreg,
+                                           dq, neg_lse, delta, t * kStep, S, ii, g, c);
   };
   // Full 64-key steps carry no key mask; a partial last step runs once after the loop.
   const int Tfull = S / kStep;
@@ -718,9 +674,6 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
     else
       step(t, kBuf0, kTail);
   }
-
-  __syncthreads();
-  for (int r = (T - 1) * kStep + tid; r < rlen; r += K::NT) prow[r] = ring_take<NW>(ring, r & (RING - 1), false);
 
   if (qvalid) {
     const int64_t qbase = (tok0 + qi) * ldd + (int64_t)h * D;
@@ -739,17 +692,76 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   }
 }
 
-// ---------------------------------------------------------- backward: dK, dV
+// ---------------------------------------------------------- backward: dK, dV, dpd
+// dpd is reduced along the diagonals inside the dK/dV kernel, in LDS, with no [B,H,S,S]
+// buffer. The workgroup diagonal of lane kk (key j_wg + kk) and query i is
+// r = kk - i + S - 1 (dpd index r + j_wg, 0 <= r < S + ROWS - 1). In a step, register pair
+// p of row group a of query block qb holds ds at the consecutive diagonals r_s, r_s + 1
+// with r_s = r0 - (8a + 32qb + 2p), r0 = kk + S - 2 - 4g - 64t, so one 64-bit
+// read-modify-write adds both. Each (wave, half-wave) owns 2 ring copies and lane kk uses
+// copy (kk + S) & 1: within one instruction the lanes of a copy are 2 apart in kk and hit
+// disjoint slot pairs, and a wave's LDS operations complete in order, so the plain
+// read-modify-write is exact and deterministic (LDS float atomics are ~30x slower here).
+// Slots: a pair starts at ((r0 & 255) + 64 + copy) - (8a + 32qb + 2p), never wrapping, so
+// diagonal r sits at (r & 255) + 64 + copy, or (r & 255) - 192 + copy when r & 255 >= 192,
+// or 320 + copy when r & 255 == 0. A step touches 191 diagonals and the 64 that can get no
+// further contribution are folded at the next step into one partial row per key block, so
+// at most 255 are live: distinct mod 256. Copy 1 sits 30 (S even) or 32 (S odd) floats past
+// a 64-float boundary, which puts the 32 lanes of one b64 access phase on distinct banks;
+// the copies of (wave, half) index wg are skewed by 8 wg floats, which puts the 4 lanes
+// folding one diagonal (wg = 2 part + q) on distinct banks too.
+constexpr int kRingSlots = 384;  // floats per ring copy (>= 322 + 32 + 8, a multiple of 64)
+constexpr int kZeroSlot = 336;   // a slot no read-modify-write reaches: always 0
+__device__ __forceinline__ int ring_base(int wg, int k, int ring1) {
+  return (2 * wg + k) * kRingSlots + 8 * wg + (k ? ring1 + 1 : 0);
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  return v;
+}
+
+// Fold diagonal r >= 0 out of the rings (4 lanes per diagonal, lane part = tid % 4 takes
+// the rings of (wave, half) 2 part and 2 part + 1) and clear its slots; every lane of the
+// quad returns the same fixed-order sum. Branch-free: the second slot is the B or C alias
+// where r has one, else the zero slot, and all reads are issued before the clears.
+__device__ __forceinline__ float ring_fold(float* ring, int r, int ring1) {
+  const int part = threadIdx.x & 3;
+  const int rr = r & 255;
+  const int sa = rr + 64;
+  const int sb = rr >= 192 ? rr - 192 : (rr == 0 ? 320 : kZeroSlot);
+  float* base[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) base[e] = ring + ring_base(2 * part + (e >> 1), e & 1, ring1);
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[2 * e] = base[e][sa];
+    x[2 * e + 1] = base[e][sb];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) base[e][sa] = base[e][sb] = 0.f;
+  float v = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v += x[e];
+  return quad_sum(v);
+}
 template <int DP, int NW>
 __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd, int S, int H,
-    int D, Fold f, float scale) {
+    const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd,
+    float* __restrict__ part, int S, int H, int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
+  static_assert(K::ROWS <= 128, "the dpd rings hold 256 live diagonals");
+  static_assert(K::NT == 256, "the ring fold maps 4 lanes to each of 64 diagonals");
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
+  constexpr int RINGF = 2 * 2 * NW * kRingSlots + 64;  // + the largest skew and copy-1 shift
+  __shared__ __attribute__((aligned(16))) float ring[RINGF];
+  __shared__ __attribute__((aligned(16))) float sink[kRingSlots];  // ds of keys past S
   __shared__ __attribute__((aligned(16))) uint16_t Qs[2 * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t Os[2 * TILE];
   __shared__ __attribute__((aligned(16))) float Lq[2 * kStep];
@@ -762,7 +774,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   const int nkb = (S + K::ROWS - 1) / K::ROWS;
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
   const int bh = tile / nkb, b = bh / H, h = bh - b * H;
-  const int j_wg = (tile - bh * nkb) * K::ROWS;
+  const int kblk = tile - bh * nkb;
+  const int j_wg = kblk * K::ROWS;
   const int kk = wave * 32 + l32;
   const int kj = j_wg + kk;
   const bool kvalid = kj < S;
@@ -791,6 +804,14 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 #pragma unroll
     for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
+  // dpd rings (published by the first step's barrier) and this key block's partial row.
+  for (int e = tid; e < RINGF; e += K::NT) ring[e] = 0.f;
+  const int ring1 = (S & 1) ? 32 : 30;
+  const int rcopy = (kk + S) & 1;
+  // Keys past S have p != 0 (their bias is real) but no dpd term: their ds go to a sink.
+  float* myring = kvalid ? ring + ring_base(2 * wave + g, rcopy, ring1) : sink;
+  float* prow = part + ((int64_t)bh * nkb + kblk) * (S + K::ROWS);
+
   uint32_t qoff[Dma<DP, K::NT>::GPT], ooff[Dma<DP, K::NT>::GPT];
   dma_offsets<DP, K::NT>(qoff, ld, D);
   dma_offsets<DP, K::NT>(ooff, HD, D);
@@ -800,7 +821,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   // Per-query statistics of the step, loaded one step ahead: wave 0 lse, wave 1 delta
   // (zero past S through the buffer range check). Stashed as -lse, with -inf past S, which
   // makes those rows' p = exp2(acc c - lse) exactly 0 (acc is finite there).
-  const rsrc_t rstat = make_rsrc(wave == 0 ? lse_bh : dl_bh, (uint32_t)S * 4u);
+  const rsrc_t rstat =
+      make_rsrc(__builtin_amdgcn_readfirstlane(wave) == 0 ? lse_bh : dl_bh, (uint32_t)S * 4u);
   auto stats = [&](int i0) {
     if (wave < 2) sst = bload4(rstat, opaque((uint32_t)(i0 + lane) * 4u));
   };
@@ -834,6 +856,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       load_bias<NW>(bst, pdh, npd, rb0 - i1, -1);
       stats(i1);
     }
+    const int rp0 = ((kk + S - 2 - 4 * g - kStep * t) & 255) + 64;  // slot of r0 in this copy
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       f32x16 acc = read_bias16<NW>(Bb, (K::ROWS - 1) - kk + qb * 32 + 4 * g), accp;
@@ -857,6 +880,20 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
           ds[r] = pv * (accp[r] - d4[b4]);
         }
       }
+      // dpd: pair p of row group a holds diagonals r_s (register 4a + 2p + 1) and r_s + 1
+      // (register 4a + 2p); the accesses are volatile so they stay in program order.
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          typedef float f32x2 __attribute__((ext_vector_type(2)));
+          typedef __attribute__((address_space(3))) f32x2 lds_f32x2;
+          volatile lds_f32x2* rs = (volatile lds_f32x2*)(myring + rp0 - (8 * a + 32 * qb + 2 * pp));
+          f32x2 v = *rs;
+          v.x += ds[4 * a + 2 * pp + 1];
+          v.y += ds[4 * a + 2 * pp];
+          *rs = v;
+        }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const u32x4 pa = pack8(&p[8 * u]);
@@ -866,6 +903,14 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
           dv[db] = mfma32x32x16(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
           dk[db] = mfma32x32x16(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
         }
+      }
+      // Diagonals [S + 63 - 64(t-1), S + 126 - 64(t-1)] got their last ds in step t-1 (step
+      // t touches [S - 64 - 64t, S + 62 - 64(t-1)], distinct mod 256): fold them into the
+      // partial row (r > 0 here), mid-step so the wait overlaps the MFMAs in flight.
+      if (qb == 0 && t > 0) {
+        const int r = S + 63 - kStep * (t - 1) + (tid >> 2);
+        const float v = ring_fold(ring, r, ring1);
+        if ((tid & 3) == 0) prow[r] = v;
       }
     }
   };
@@ -877,6 +922,17 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
     step(t + 1, kBuf1);
   }
   if (t < T) step(t, kBuf0);
+
+  // Fold every diagonal still in the rings: [0, S + 126 - 64(T-1)].
+  __syncthreads();
+  const int nrem = S + K::ROWS - 1 - kStep * (T - 1);
+  for (int r0 = 0; r0 < nrem; r0 += kStep) {
+    const int r = r0 + (tid >> 2);
+    if (r < nrem) {  // uniform per quad
+      const float v = ring_fold(ring, r, ring1);
+      if ((tid & 3) == 0) prow[r] = v;
+    }
+  }
 
   // D layout: lane = head dim d (n), register r = key 8(r/4) + 4g + r%4 of this wave.
 #pragma unroll
@@ -896,9 +952,9 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   }
 }
 
-// dpd[h, k] = sum over b and query blocks of the partial rows, fixed order.
-// Block: 64 diagonals (lane) of head h; the 4 waves take every 4th (b, query
-// block) term, then the 4 wave sums are added in wave order.
+// dpd[h, k] = sum over b and key blocks of the partial rows (row of key block kb holds
+// k - rows kb), fixed order. Block: 64 diagonals (lane) of head h; the 4 waves take every
+// 4th (b, key block) term, then the 4 wave sums are added in wave order.
 __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict__ part,
                                                          float* __restrict__ dpd, int B, int S,
                                                          int H, int nqb, int rows) {
@@ -914,9 +970,9 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
     const int terms = B * nqb;
 #pragma unroll 4
     for (int e = wave; e < terms; e += 4) {
-      const int b = e / nqb, qb = e - b * nqb;
-      const int r = k - S + rows + rows * qb;
-      if (r >= 0 && r < rlen) acc += part[((int64_t)(b * H + h) * nqb + qb) * RS + r];
+      const int b = e / nqb, kb = e - b * nqb;
+      const int r = k - rows * kb;
+      if (r >= 0 && r < rlen) acc += part[((int64_t)(b * H + h) * nqb + kb) * RS + r];
     }
   }
   s[wave][lane] = acc;
@@ -957,12 +1013,13 @@ Fold fold_scale(float scale) {
 
 int padded_dim(int D) { return (D + 15) / 16 * 16; }
 
-constexpr int kDqRows = Blk<kDqNW>::ROWS;
+constexpr int kKvRows = Blk<kDkdvNW>::ROWS;
 
 size_t ws_delta_bytes(int B, int S, int H) { return align256((size_t)B * H * S * sizeof(float)); }
+// One dpd partial row of S + rows floats per (b, h, key block).
 size_t ws_part_bytes(int B, int S, int H) {
-  const size_t nqb = (size_t)ceil_div(S, kDqRows);
-  return align256((size_t)B * H * nqb * (size_t)(S + kDqRows) * sizeof(float));
+  const size_t nkb = (size_t)ceil_div(S, kKvRows);
+  return align256((size_t)B * H * nkb * (size_t)(S + kKvRows) * sizeof(float));
 }
 
 template <int DP>
@@ -983,16 +1040,16 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   float* delta = static_cast<float*>(ws);
   float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_delta_bytes(B, S, H));
   const int nqb = (int)ceil_div(S, KQ::ROWS);
+  const int nkb = (int)ceil_div(S, KK::ROWS);
   hipLaunchKernelGGL((relpos_bwd_dq_kernel<DP, kDqNW>), dim3((unsigned)(nqb * B * H)),
                      dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
-                     lse, delta, part, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
-  hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DP, kDkdvNW>),
-                     dim3((unsigned)(ceil_div(S, KK::ROWS) * B * H)), dim3(KK::NT), 0, st,
-                     (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse, (const float*)delta,
-                     (uint16_t*)dqkv, ldd, S, H, D, f, scale);
+                     lse, delta, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
+  hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DP, kDkdvNW>), dim3((unsigned)(nkb * B * H)),
+                     dim3(KK::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
+                     (const float*)delta, (uint16_t*)dqkv, ldd, part, S, H, D, f, scale);
   const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
   hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S, H,
-                     nqb, KQ::ROWS);
+                     nkb, KK::ROWS);
 }
 
 }  // namespace
