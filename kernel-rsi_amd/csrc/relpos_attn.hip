@@ -698,23 +698,27 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
 // r = kk - i + S - 1 (dpd index r + j_wg, 0 <= r < S + ROWS - 1). In a step, register pair
 // p of row group a of query block qb holds ds at the consecutive diagonals r_s, r_s + 1
 // with r_s = r0 - (8a + 32qb + 2p), r0 = kk + S - 2 - 4g - 64t, so one 64-bit
-// read-modify-write adds both. Each (wave, half-wave) owns 2 ring copies and lane kk uses
+// read-modify-write adds both. Each (wave, half-wave) owns 2 ring copies and key kk uses
 // copy (kk + S) & 1: within one instruction the lanes of a copy are 2 apart in kk and hit
 // disjoint slot pairs, and a wave's LDS operations complete in order, so the plain
 // read-modify-write is exact and deterministic (LDS float atomics are ~30x slower here).
+// Bank rules measured on gfx950: b64 reads are served 32 lanes at a time over 64 banks,
+// b64 writes 16 lanes at a time over 32 banks, b32 accesses 32 lanes at a time over 32
+// banks. Column l of the wave's score tile holds key kperm(l) = 2 (l % 16) + l / 16, so a
+// 16-lane write phase touches one copy only (32 contiguous floats).
 // Slots: a pair starts at ((r0 & 255) + 64 + copy) - (8a + 32qb + 2p), never wrapping, so
 // diagonal r sits at (r & 255) + 64 + copy, or (r & 255) - 192 + copy when r & 255 >= 192,
 // or 320 + copy when r & 255 == 0. A step touches 191 diagonals and the 64 that can get no
 // further contribution are folded at the next step into one partial row per key block, so
 // at most 255 are live: distinct mod 256. Copy 1 sits 30 (S even) or 32 (S odd) floats past
-// a 64-float boundary, which puts the 32 lanes of one b64 access phase on distinct banks;
-// the copies of (wave, half) index wg are skewed by 8 wg floats, which puts the 4 lanes
-// folding one diagonal (wg = 2 part + q) on distinct banks too.
-constexpr int kRingSlots = 384;  // floats per ring copy (>= 322 + 32 + 8, a multiple of 64)
-constexpr int kZeroSlot = 336;   // a slot no read-modify-write reaches: always 0
+// a 64-float boundary, which puts the 32 lanes of one b64 read phase on distinct banks;
+// the copies of (wave, half) index wg are skewed by 4 wg floats, which puts the 32 lanes
+// of one fold phase (8 diagonals x 4 rings wg = 2 part + q) on distinct banks too.
+constexpr int kRingSlots = 384;  // floats per ring copy (>= 322 + 32 + 4, a multiple of 64)
 __device__ __forceinline__ int ring_base(int wg, int k, int ring1) {
-  return (2 * wg + k) * kRingSlots + 8 * wg + (k ? ring1 + 1 : 0);
+  return (2 * wg + k) * kRingSlots + 4 * wg + (k ? ring1 + 1 : 0);
 }
+__device__ __forceinline__ int kperm(int l) { return 2 * (l & 15) + (l >> 4); }
 
 __device__ __forceinline__ float quad_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
@@ -725,23 +729,30 @@ __device__ __forceinline__ float quad_sum(float v) {
 // Fold diagonal r >= 0 out of the rings (4 lanes per diagonal, lane part = tid % 4 takes
 // the rings of (wave, half) 2 part and 2 part + 1) and clear its slots; every lane of the
 // quad returns the same fixed-order sum. Branch-free: the second slot is the B or C alias
-// where r has one, else the zero slot, and all reads are issued before the clears.
-__device__ __forceinline__ float ring_fold(float* ring, int r, int ring1) {
+// where r has one, else this lane's own always-zero float in zl, and all reads are issued
+// before the clears.
+__device__ __forceinline__ float ring_fold(float* ring, float* zl, int r, int ring1) {
   const int part = threadIdx.x & 3;
   const int rr = r & 255;
   const int sa = rr + 64;
-  const int sb = rr >= 192 ? rr - 192 : (rr == 0 ? 320 : kZeroSlot);
-  float* base[4];
+  const bool alias = rr >= 192 || rr == 0;
+  const int sb = rr == 0 ? 320 : rr - 192;
+  float* pa[4];
+  float* pb[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) base[e] = ring + ring_base(2 * part + (e >> 1), e & 1, ring1);
+  for (int e = 0; e < 4; ++e) {
+    float* base = ring + ring_base(2 * part + (e >> 1), e & 1, ring1);
+    pa[e] = base + sa;
+    pb[e] = alias ? base + sb : zl;
+  }
   float x[8];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    x[2 * e] = base[e][sa];
-    x[2 * e + 1] = base[e][sb];
+    x[2 * e] = *pa[e];
+    x[2 * e + 1] = *pb[e];
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) base[e][sa] = base[e][sb] = 0.f;
+  for (int e = 0; e < 4; ++e) *pa[e] = *pb[e] = 0.f;
   float v = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v += x[e];
@@ -762,6 +773,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   constexpr int RINGF = 2 * 2 * NW * kRingSlots + 64;  // + the largest skew and copy-1 shift
   __shared__ __attribute__((aligned(16))) float ring[RINGF];
   __shared__ __attribute__((aligned(16))) float sink[kRingSlots];  // ds of keys past S
+  __shared__ __attribute__((aligned(16))) float zeros[64];          // one always-0 float per lane
   __shared__ __attribute__((aligned(16))) uint16_t Qs[2 * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t Os[2 * TILE];
   __shared__ __attribute__((aligned(16))) float Lq[2 * kStep];
@@ -776,7 +788,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   const int bh = tile / nkb, b = bh / H, h = bh - b * H;
   const int kblk = tile - bh * nkb;
   const int j_wg = kblk * K::ROWS;
-  const int kk = wave * 32 + l32;
+  const int kk = wave * 32 + kperm(l32);  // this lane's key (score tile column l32)
   const int kj = j_wg + kk;
   const bool kvalid = kj < S;
   const int64_t tok0 = (int64_t)b * S;
@@ -806,6 +818,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 
   // dpd rings (published by the first step's barrier) and this key block's partial row.
   for (int e = tid; e < RINGF; e += K::NT) ring[e] = 0.f;
+  if (tid < 64) zeros[tid] = 0.f;
+  float* zl = zeros + lane;
   const int ring1 = (S & 1) ? 32 : 30;
   const int rcopy = (kk + S) & 1;
   // Keys past S have p != 0 (their bias is real) but no dpd term: their ds go to a sink.
@@ -909,7 +923,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       // partial row (r > 0 here), mid-step so the wait overlaps the MFMAs in flight.
       if (qb == 0 && t > 0) {
         const int r = S + 63 - kStep * (t - 1) + (tid >> 2);
-        const float v = ring_fold(ring, r, ring1);
+        const float v = ring_fold(ring, zl, r, ring1);
         if ((tid & 3) == 0) prow[r] = v;
       }
     }
@@ -929,19 +943,20 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   for (int r0 = 0; r0 < nrem; r0 += kStep) {
     const int r = r0 + (tid >> 2);
     if (r < nrem) {  // uniform per quad
-      const float v = ring_fold(ring, r, ring1);
+      const float v = ring_fold(ring, zl, r, ring1);
       if ((tid & 3) == 0) prow[r] = v;
     }
   }
 
-  // D layout: lane = head dim d (n), register r = key 8(r/4) + 4g + r%4 of this wave.
+  // D layout: lane = head dim d (n), register r = tile row 8(r/4) + 4g + r%4, which holds
+  // key kperm(row) of this wave.
 #pragma unroll
   for (int db = 0; db < G::DB; ++db) {
     const int d = db * 32 + l32;
     if (d < D) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = j_wg + wave * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int key = j_wg + wave * 32 + kperm(8 * (r >> 2) + 4 * g + (r & 3));
         if (key < S) {
           uint16_t* rowp = dqkv + (tok0 + key) * ldd + HD + (int64_t)h * D + d;
           rowp[0] = f32_to_bf16(dk[db][r] * scale);
