@@ -694,29 +694,30 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
 
 // ---------------------------------------------------------- backward: dK, dV, dpd
 // dpd is reduced along the diagonals inside the dK/dV kernel, in LDS, with no [B,H,S,S]
-// buffer. The workgroup diagonal of lane kk (key j_wg + kk) and query i is
+// buffer. The workgroup diagonal of key kk (key j_wg + kk) and query i is
 // r = kk - i + S - 1 (dpd index r + j_wg, 0 <= r < S + ROWS - 1). In a step, register pair
 // p of row group a of query block qb holds ds at the consecutive diagonals r_s, r_s + 1
-// with r_s = r0 - (8a + 32qb + 2p), r0 = kk + S - 2 - 4g - 64t, so one 64-bit
+// with r_s = r0 - d, r0 = kk + S - 2 - 4g - 64t, d = 8a + 32qb + 2p, so one 64-bit
 // read-modify-write adds both. Each (wave, half-wave) owns 2 ring copies and key kk uses
-// copy (kk + S) & 1: within one instruction the lanes of a copy are 2 apart in kk and hit
-// disjoint slot pairs, and a wave's LDS operations complete in order, so the plain
+// copy k = (kk + S) & 1: within one instruction the lanes of a copy are 2 apart in kk and
+// hit disjoint slot pairs, and a wave's LDS operations complete in order, so the plain
 // read-modify-write is exact and deterministic (LDS float atomics are ~30x slower here).
+// Copy k keeps diagonal r at slot (r - k) & 255, or 256 above it: the pair of r_s starts
+// at slot ((r0 - k - 58) & 255) + 58 - d, which is even (r_s - k is) and never wraps. A
+// step touches 191 diagonals and the 64 that can get no further contribution are folded
+// at the next step into one partial row per key block, so at most 255 are live: distinct
+// mod 256. The fold reads and clears both slots of a copy with one read2st64/write2st64.
 // Bank rules measured on gfx950: b64 reads are served 32 lanes at a time over 64 banks,
 // b64 writes 16 lanes at a time over 32 banks, b32 accesses 32 lanes at a time over 32
 // banks. Column l of the wave's score tile holds key kperm(l) = 2 (l % 16) + l / 16, so a
-// 16-lane write phase touches one copy only (32 contiguous floats).
-// Slots: a pair starts at ((r0 & 255) + 64 + copy) - (8a + 32qb + 2p), never wrapping, so
-// diagonal r sits at (r & 255) + 64 + copy, or (r & 255) - 192 + copy when r & 255 >= 192,
-// or 320 + copy when r & 255 == 0. A step touches 191 diagonals and the 64 that can get no
-// further contribution are folded at the next step into one partial row per key block, so
-// at most 255 are live: distinct mod 256. Copy 1 sits 30 (S even) or 32 (S odd) floats past
-// a 64-float boundary, which puts the 32 lanes of one b64 read phase on distinct banks;
-// the copies of (wave, half) index wg are skewed by 4 wg floats, which puts the 32 lanes
-// of one fold phase (8 diagonals x 4 rings wg = 2 part + q) on distinct banks too.
-constexpr int kRingSlots = 384;  // floats per ring copy (>= 322 + 32 + 4, a multiple of 64)
-__device__ __forceinline__ int ring_base(int wg, int k, int ring1) {
-  return (2 * wg + k) * kRingSlots + 4 * wg + (k ? ring1 + 1 : 0);
+// 16-lane write phase touches one copy only (32 contiguous floats); copy 1 sits 32 (S even)
+// or 34 (S odd) floats past a 64-float boundary, which puts the two copies of a 32-lane
+// read phase on distinct banks; the copies of (wave, half) index wg are skewed by 4 wg
+// floats, which puts the 32 lanes of one fold phase (8 diagonals x 4 rings) on distinct
+// banks.
+constexpr int kRingSlots = 576;  // floats per ring copy (>= 512 + 34 + 28, a multiple of 64)
+__device__ __forceinline__ int ring_base(int wg, int k, int off1) {
+  return (2 * wg + k) * kRingSlots + 4 * wg + (k ? off1 : 0);
 }
 __device__ __forceinline__ int kperm(int l) { return 2 * (l & 15) + (l >> 4); }
 
@@ -728,31 +729,21 @@ __device__ __forceinline__ float quad_sum(float v) {
 
 // Fold diagonal r >= 0 out of the rings (4 lanes per diagonal, lane part = tid % 4 takes
 // the rings of (wave, half) 2 part and 2 part + 1) and clear its slots; every lane of the
-// quad returns the same fixed-order sum. Branch-free: the second slot is the B or C alias
-// where r has one, else this lane's own always-zero float in zl, and all reads are issued
-// before the clears.
-__device__ __forceinline__ float ring_fold(float* ring, float* zl, int r, int ring1) {
+// quad returns the same fixed-order sum. All reads are issued before the clears.
+__device__ __forceinline__ float ring_fold(float* ring, int r, int off1) {
   const int part = threadIdx.x & 3;
-  const int rr = r & 255;
-  const int sa = rr + 64;
-  const bool alias = rr >= 192 || rr == 0;
-  const int sb = rr == 0 ? 320 : rr - 192;
   float* pa[4];
-  float* pb[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    float* base = ring + ring_base(2 * part + (e >> 1), e & 1, ring1);
-    pa[e] = base + sa;
-    pb[e] = alias ? base + sb : zl;
-  }
+  for (int e = 0; e < 4; ++e)
+    pa[e] = ring + ring_base(2 * part + (e >> 1), e & 1, off1) + ((r - (e & 1)) & 255);
   float x[8];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    x[2 * e] = *pa[e];
-    x[2 * e + 1] = *pb[e];
+    x[2 * e] = pa[e][0];
+    x[2 * e + 1] = pa[e][256];
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) *pa[e] = *pb[e] = 0.f;
+  for (int e = 0; e < 4; ++e) pa[e][0] = pa[e][256] = 0.f;
   float v = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) v += x[e];
@@ -770,10 +761,9 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   static_assert(K::NT == 256, "the ring fold maps 4 lanes to each of 64 diagonals");
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
-  constexpr int RINGF = 2 * 2 * NW * kRingSlots + 64;  // + the largest skew and copy-1 shift
+  constexpr int RINGF = 2 * 2 * NW * kRingSlots;
   __shared__ __attribute__((aligned(16))) float ring[RINGF];
-  __shared__ __attribute__((aligned(16))) float sink[kRingSlots];  // ds of keys past S
-  __shared__ __attribute__((aligned(16))) float zeros[64];          // one always-0 float per lane
+  __shared__ __attribute__((aligned(16))) float sink[320];  // ds of keys past S
   __shared__ __attribute__((aligned(16))) uint16_t Qs[2 * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t Os[2 * TILE];
   __shared__ __attribute__((aligned(16))) float Lq[2 * kStep];
@@ -818,12 +808,10 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 
   // dpd rings (published by the first step's barrier) and this key block's partial row.
   for (int e = tid; e < RINGF; e += K::NT) ring[e] = 0.f;
-  if (tid < 64) zeros[tid] = 0.f;
-  float* zl = zeros + lane;
-  const int ring1 = (S & 1) ? 32 : 30;
+  const int off1 = (S & 1) ? 34 : 32;
   const int rcopy = (kk + S) & 1;
   // Keys past S have p != 0 (their bias is real) but no dpd term: their ds go to a sink.
-  float* myring = kvalid ? ring + ring_base(2 * wave + g, rcopy, ring1) : sink;
+  float* myring = kvalid ? ring + ring_base(2 * wave + g, rcopy, off1) : sink;
   float* prow = part + ((int64_t)bh * nkb + kblk) * (S + K::ROWS);
 
   uint32_t qoff[Dma<DP, K::NT>::GPT], ooff[Dma<DP, K::NT>::GPT];
@@ -834,7 +822,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   const int T = (S + kStep - 1) / kStep;
   // Per-query statistics of the step, loaded one step ahead: wave 0 lse, wave 1 delta
   // (zero past S through the buffer range check). Stashed as -lse, with -inf past S, which
-  // makes those rows' p = exp2(acc c - lse) exactly 0 (acc is finite there).
+  // makes those rows' p = exp2(acc c - lse) exactly 0 (acc is finite there), and -delta.
   const rsrc_t rstat =
       make_rsrc(__builtin_amdgcn_readfirstlane(wave) == 0 ? lse_bh : dl_bh, (uint32_t)S * 4u);
   auto stats = [&](int i0) {
@@ -861,7 +849,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
     if (wave == 0)
       Lq[B * kStep + lane] = t * kStep + lane < S ? -sst : -INFINITY;
     else if (wave == 1)
-      Dq[B * kStep + lane] = sst;
+      Dq[B * kStep + lane] = -sst;
     drain_and_sync();
     if (t + 1 < T) {
       const int i1 = (t + 1) * kStep;
@@ -870,12 +858,17 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       load_bias<NW>(bst, pdh, npd, rb0 - i1, -1);
       stats(i1);
     }
-    const int rp0 = ((kk + S - 2 - 4 * g - kStep * t) & 255) + 64;  // slot of r0 in this copy
+    const int rp0 = ((kk + S - 2 - 4 * g - kStep * t - rcopy - 58) & 255) + 58;  // slot of r0
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
+      // dP starts at -D of its row, so the product below is ds / p directly.
       f32x16 acc = read_bias16<NW>(Bb, (K::ROWS - 1) - kk + qb * 32 + 4 * g), accp;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) accp[r] = 0.f;
+      for (int a = 0; a < 4; ++a) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(Db + qb * 32 + 8 * a + 4 * g);
+#pragma unroll
+        for (int b4 = 0; b4 < 4; ++b4) accp[4 * a + b4] = d4[b4];
+      }
 #pragma unroll
       for (int s = 0; s < G::KS; ++s) {
         acc = mfma32x32x16(row_operand<DP>(Qb, L, qb * 32, s), kreg[s], acc);
@@ -885,13 +878,12 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const f32x4 nl4 = *reinterpret_cast<const f32x4*>(Lb + qb * 32 + 8 * a + 4 * g);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(Db + qb * 32 + 8 * a + 4 * g);
 #pragma unroll
         for (int b4 = 0; b4 < 4; ++b4) {
           const int r = 4 * a + b4;
           const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], c, nl4[b4]));
           p[r] = pv;
-          ds[r] = pv * (accp[r] - d4[b4]);
+          ds[r] = pv * accp[r];
         }
       }
       // dpd: pair p of row group a holds diagonals r_s (register 4a + 2p + 1) and r_s + 1
@@ -923,7 +915,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       // partial row (r > 0 here), mid-step so the wait overlaps the MFMAs in flight.
       if (qb == 0 && t > 0) {
         const int r = S + 63 - kStep * (t - 1) + (tid >> 2);
-        const float v = ring_fold(ring, zl, r, ring1);
+        const float v = ring_fold(ring, r, off1);
         if ((tid & 3) == 0) prow[r] = v;
       }
     }
@@ -943,7 +935,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   for (int r0 = 0; r0 < nrem; r0 += kStep) {
     const int r = r0 + (tid >> 2);
     if (r < nrem) {  // uniform per quad
-      const float v = ring_fold(ring, zl, r, ring1);
+      const float v = ring_fold(ring, r, off1);
       if ((tid & 3) == 0) prow[r] = v;
     }
   }
