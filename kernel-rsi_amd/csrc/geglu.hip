@@ -79,7 +79,8 @@ __global__ __launch_bounds__(kThreads) void geglu_fwd_vec(const uint16_t* __rest
     unpack8(bv, b);
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = round_bf16(gelu_fwd<TANH>(a[j])) * b[j];
-    reinterpret_cast<u32x4*>(out + r * (int64_t)f)[c] = pack8(o);
+    // Streamed out once: a non-temporal store.
+    __builtin_nontemporal_store(pack8(o), &reinterpret_cast<u32x4*>(out + r * (int64_t)f)[c]);
   }
 }
 
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(kThreads) void geglu_bwd_vec(const uint16_t* __rest
       da[j] = dgel * d;
     }
     u32x4* dr = reinterpret_cast<u32x4*>(du + r * 2 * (int64_t)f);
-    dr[c] = pack8(da);
-    dr[f8 + c] = pack8(db);
+    __builtin_nontemporal_store(pack8(da), &dr[c]);
+    __builtin_nontemporal_store(pack8(db), &dr[f8 + c]);
   }
 }
 

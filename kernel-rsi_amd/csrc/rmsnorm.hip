@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const uint16_t* __restri
       unpack8(wr[c], wf);
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] = wf[j] * round_bf16(xf[j] * r);
-      yr[c] = pack8(o);
+      __builtin_nontemporal_store(pack8(o), &yr[c]);  // streamed out, not re-read
     }
   }
 }
@@ -149,21 +149,33 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
 
   const int64_t groups_total = (int64_t)gridDim.x * RPB;
   const int64_t iters = (rows + groups_total - 1) / groups_total;
-  for (int64_t it = 0; it < iters; ++it) {
-    const int64_t row = (it * gridDim.x + blockIdx.x) * RPB + grp;
+  // The next row's g, x and rstd are requested before this row is reduced and written, so
+  // every wave keeps one row of loads in flight. g, x and dx are streamed once: non-temporal
+  // loads and stores keep them from displacing other lines in the caches.
+  u32x4 gv[VPT], xv[VPT];
+  float r;
+  auto fetch = [&](int64_t row, u32x4* gq, u32x4* xq, float& rq) {
     const bool live = row < rows;
     const int64_t base = (live ? row : 0) * (int64_t)n;
     const u32x4* gr = reinterpret_cast<const u32x4*>(g + base);
     const u32x4* xr = reinterpret_cast<const u32x4*>(x + base);
-    u32x4 gv[VPT], xv[VPT];
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int c = gtid + k * GT;
       const bool ok = live && c < nch;
-      gv[k] = ok ? gr[c] : u32x4{0u, 0u, 0u, 0u};
-      xv[k] = ok ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+      gq[k] = ok ? __builtin_nontemporal_load(&gr[c]) : u32x4{0u, 0u, 0u, 0u};
+      xq[k] = ok ? __builtin_nontemporal_load(&xr[c]) : u32x4{0u, 0u, 0u, 0u};
     }
-    const float r = live ? rstd[row] : 0.f;
+    rq = live ? rstd[row] : 0.f;
+  };
+  int64_t row = (int64_t)blockIdx.x * RPB + grp;
+  fetch(row, gv, xv, r);
+  for (int64_t it = 0; it < iters; ++it, row += groups_total) {
+    const bool live = row < rows;
+    const int64_t base = (live ? row : 0) * (int64_t)n;
+    u32x4 gn[VPT], xn[VPT];
+    float rn = 0.f;
+    if (it + 1 < iters) fetch(row + groups_total, gn, xn, rn);
     float sdot = 0.f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
@@ -202,9 +214,17 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
             const float dn = round_bf16(gf[j] * wv[k][j]);
             o[j] = r * dn - (xf[j] * r3) * sn;
           }
-          dxr[c] = pack8(o);
+          __builtin_nontemporal_store(pack8(o), &dxr[c]);
         }
       }
+    }
+    if (it + 1 < iters) {
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        gv[k] = gn[k];
+        xv[k] = xn[k];
+      }
+      r = rn;
     }
   }
 
@@ -351,7 +371,12 @@ int pick_vpt(int n, int wpr) {
   return v;
 }
 
-int pick_wpr(int n) { return n <= 4096 ? 1 : (n <= 8192 ? 2 : 4); }
+// Rows wider than 2048 take a whole workgroup (4 waves): fewer registers per
+// lane, more waves in flight.
+int pick_wpr(int n) { return n <= 2048 ? 1 : 4; }
+// The backward holds w, its dw share and two rows of g and x per lane, so it
+// spreads a row over more waves: at most 2 chunks per lane up to n = 4096.
+int pick_wpr_bwd(int n) { return n <= 1024 ? 1 : (n <= 2048 ? 2 : 4); }
 
 // Rows per block of the scalar dw kernel: at least kScalarRowChunk, and few
 // enough blocks that the partials stay within kBwdMaxBlocks rows.
@@ -363,7 +388,7 @@ int64_t scalar_chunk(int64_t rows) {
 // Rows of partials the backward writes before the column sums (<= 512).
 int64_t bwd_partial_rows(int64_t rows, int n, bool vec) {
   if (vec) {
-    const int64_t rpb = kWavesPerBlock / pick_wpr(n);
+    const int64_t rpb = kWavesPerBlock / pick_wpr_bwd(n);
     const int64_t b = ceil_div(rows, rpb);
     return b < kBwdMaxBlocks ? b : kBwdMaxBlocks;
   }
@@ -407,8 +432,8 @@ int krsi_rmsnorm_fwd_bf16(const void* x, const void* w, void* y, float* rstd, in
     launch_fwd<W, V>(x, w, y, rstd, rows, n, eps, st);   \
     return launch_status();                              \
   }
-    KRSI_FWD_CASE(1, 1) KRSI_FWD_CASE(1, 2) KRSI_FWD_CASE(1, 4) KRSI_FWD_CASE(1, 8)
-    KRSI_FWD_CASE(2, 8) KRSI_FWD_CASE(4, 8)
+    KRSI_FWD_CASE(1, 1) KRSI_FWD_CASE(1, 2) KRSI_FWD_CASE(1, 4)
+    KRSI_FWD_CASE(4, 2) KRSI_FWD_CASE(4, 4) KRSI_FWD_CASE(4, 8)
 #undef KRSI_FWD_CASE
     return KRSI_ERR_UNSUPPORTED;
   }
@@ -439,7 +464,7 @@ int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const flo
   float* part = static_cast<float*>(workspace);
   int64_t p1 = 0;
   if (vec_ok(n, {g, x, w, dx})) {
-    const int wpr = pick_wpr(n);
+    const int wpr = pick_wpr_bwd(n);
     const int vpt = pick_vpt(n, wpr);
     bool done = false;
 #define KRSI_BWD_CASE(W, V)                                            \
@@ -447,8 +472,8 @@ int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const flo
     p1 = launch_bwd<W, V>(g, x, w, rstd, dx, part, rows, n, st);       \
     done = true;                                                       \
   }
-    KRSI_BWD_CASE(1, 1) KRSI_BWD_CASE(1, 2) KRSI_BWD_CASE(1, 4) KRSI_BWD_CASE(1, 8)
-    KRSI_BWD_CASE(2, 8) KRSI_BWD_CASE(4, 8)
+    KRSI_BWD_CASE(1, 1) KRSI_BWD_CASE(1, 2) KRSI_BWD_CASE(2, 1) KRSI_BWD_CASE(2, 2)
+    KRSI_BWD_CASE(4, 1) KRSI_BWD_CASE(4, 2) KRSI_BWD_CASE(4, 4) KRSI_BWD_CASE(4, 8)
 #undef KRSI_BWD_CASE
     if (!done) return KRSI_ERR_UNSUPPORTED;
   } else {
