@@ -39,13 +39,30 @@ __device__ __forceinline__ float tanh_via_exp(float z) {
   return 1.0f - 2.0f / (e + 1.0f);
 }
 
+// erf by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26:
+// erf(x) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-x^2}, t = 1 / (1 + p x), x >= 0,
+// absolute error <= 1.5e-7 (<= 6e-7 evaluated in fp32), far below a bf16 ulp of the output.
+// Returns erf(a / sqrt 2); ex must be e^{-a^2 / 2}, which gelu' needs as well.
+__device__ __forceinline__ float erf_as(float a, float ex) {
+  const float x = fabsf(a) * kInvSqrt2;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, x, 1.0f));
+  float q = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  q = __builtin_fmaf(q, t, 1.421413741f);
+  q = __builtin_fmaf(q, t, -0.284496736f);
+  q = __builtin_fmaf(q, t, 0.254829592f);
+  return copysignf(1.0f - q * t * ex, a);
+}
+__device__ __forceinline__ float exp_half_sq(float a) {
+  return __builtin_amdgcn_exp2f(-0.5f * kLog2e * a * a);
+}
+
 template <bool TANH>
 __device__ __forceinline__ float gelu_fwd(float a) {
   if (TANH) {
     const float z = kSqrt2OverPi * (a + kKappa * a * a * a);
     return 0.5f * a * (1.0f + tanh_via_exp(z));
   }
-  return 0.5f * a * (1.0f + erff(a * kInvSqrt2));
+  return 0.5f * a * (1.0f + erf_as(a, exp_half_sq(a)));
 }
 
 // Returns gelu(a) and writes gelu'(a) to d.
@@ -58,8 +75,9 @@ __device__ __forceinline__ float gelu_fwd_bwd(float a, float& d) {
     d = 0.5f * (1.0f + t) + 0.5f * a * (1.0f - t * t) * dz;
     return 0.5f * a * (1.0f + t);
   }
-  const float e = erff(a * kInvSqrt2);
-  const float pdf = __builtin_amdgcn_exp2f(-0.5f * a * a * kLog2e) * kInvSqrt2Pi;
+  const float ex = exp_half_sq(a);
+  const float e = erf_as(a, ex);
+  const float pdf = ex * kInvSqrt2Pi;
   d = 0.5f * (1.0f + e) + a * pdf;
   return 0.5f * a * (1.0f + e);  // the forward's expression, so bf16(gelu) matches it
 }

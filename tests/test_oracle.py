@@ -212,3 +212,21 @@ def test_kernel_emulation_is_close_to_fp32():
     k = O.relpos_kernel_emulated(qkv, pd, B, S, H, D, 0.25, dout)
     for a, b in ((k[0], r[0]), (k[1], r[2]), (k[2], r[3])):
         assert ((a.float() - b).norm() / b.norm()) < 2e-2
+
+
+def test_geglu_erf_approximation_bound():
+    """The GEGLU kernels evaluate erf with Abramowitz & Stegun 7.1.26 (constants as in
+    kernel-rsi_amd/csrc/geglu.hip `erf_as`). Evaluated in float32, as the kernel does, it must
+    stay within 6e-7 of erf everywhere (the published bound is 1.5e-7 in exact arithmetic),
+    which is ~1/6500 of a bf16 ulp at 1; a wrong coefficient or sign breaks the bound."""
+    f32 = np.float32
+    p = f32(0.3275911)
+    a1, a2, a3, a4, a5 = (f32(v) for v in (0.254829592, -0.284496736, 1.421413741, -1.453152027, 1.061405429))
+    x = np.linspace(-12.0, 12.0, 240001).astype(np.float32)
+    ax = np.abs(x)
+    t = f32(1) / (f32(1) + p * ax)
+    q = ((((a5 * t + a4) * t + a3) * t + a2) * t + a1) * t
+    y = np.copysign(f32(1) - q * np.exp(-(ax * ax)).astype(np.float32), x)
+    ref = np.array([math.erf(float(v)) for v in x])
+    assert np.abs(y.astype(np.float64) - ref).max() < 6e-7
+    assert y[0] == -1.0 and y[-1] == 1.0 and y[len(x) // 2] == 0.0
