@@ -1,0 +1,47 @@
+"""The reference's acceptance protocol on the GPU, through the library's own `selftest_autograd`
+(fp32 reference vs eager original vs kernel under one random cotangent, then the kernel under
+torch.compile(fullgraph=True); tools/common.py:476-518 in the reference), for each op, without
+timing. A graph break or a fake-tensor mismatch under compile fails the compiled check."""
+import pytest
+import torch
+
+import geglu as G
+import relpos_attention as A
+import rmsnorm as R
+from _harness import selftest_autograd
+from krsi_testutil import log, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(res):
+    assert res["pass"], res["checks"]
+    assert res["compiled"].get("pass"), res["compiled"]
+
+
+def test_rmsnorm_selftest_protocol_and_compile():
+    log("selftest_autograd rmsnorm [1024, 1152] + torch.compile(fullgraph)")
+    torch.manual_seed(0)
+    x = seeded((1024, 1152), 0)
+    w = (1 + 0.02 * seeded((1152,), 1, dtype=torch.float32)).to(torch.bfloat16)
+    _check(selftest_autograd(lambda x, w: R.rmsnorm(x, w, 1e-6), lambda x, w: R.reference(x, w, 1e-6),
+                             [x, w], time=False))
+
+
+@pytest.mark.parametrize("approximate", ["none", "tanh"])
+def test_geglu_selftest_protocol_and_compile(approximate):
+    log(f"selftest_autograd geglu [512, 2*1408] {approximate} + torch.compile(fullgraph)")
+    torch.manual_seed(0)
+    u = seeded((512, 2 * 1408), 0)
+    _check(selftest_autograd(lambda u: G.geglu(u, approximate=approximate),
+                             lambda u: G.reference(u, approximate=approximate), [u], time=False))
+
+
+def test_relpos_selftest_protocol_and_compile():
+    B, S, H, D = 2, 256, 4, 64
+    log(f"selftest_autograd relpos B{B} S{S} H{H} D{D} + torch.compile(fullgraph)")
+    torch.manual_seed(0)
+    qkv = (0.6 * seeded((B * S, 3 * H * D), 0, dtype=torch.float32)).to(torch.bfloat16)
+    pd = seeded((H, 2 * S - 1), 1, dtype=torch.float32)
+    _check(selftest_autograd(lambda q, p: A.relpos_attention(q, p, B, S, H, D, 1.0),
+                             lambda q, p: A.reference(q, p, B, S, H, D, 1.0), [qkv, pd], time=False))
