@@ -12,7 +12,13 @@
  *   - Every argument is validated before the first launch; on error nothing
  *     has been launched. The return value is KRSI_OK (0) or one of the
  *     KRSI_ERR_* codes; krsi_error_string() names it.
- *   - bf16 tensors are stored as raw 16-bit bfloat16, row-major.
+ *   - Activations (x, w, g, y, dx, dw; u, out, du; qkv, dout, out, dqkv) are
+ *     row-major in one dtype chosen by a KRSI_DTYPE_* argument: bf16 and fp16
+ *     as raw 16-bit patterns, or fp32. Every rounding point the reference
+ *     applies in its input dtype (`.to(x.dtype)`, products of two tensors of
+ *     that dtype) is applied in that dtype, round-to-nearest-even. Statistics
+ *     (rstd, lse, out32, pd, dpd) are always fp32. The *_bf16 entry points are
+ *     the same functions with dtype fixed to KRSI_DTYPE_BF16.
  *   - Stateless and reentrant: any host thread may call, ordering is by stream.
  */
 #ifndef KRSI_H_
@@ -25,7 +31,13 @@
 extern "C" {
 #endif
 
-#define KRSI_ABI_VERSION 1
+#define KRSI_ABI_VERSION 2
+
+/* Activation dtypes. The reference's Triton kernels are dtype-generic; the
+ * attention entry points take bf16 and fp16 (fp32 qkv: KRSI_ERR_UNSUPPORTED). */
+#define KRSI_DTYPE_BF16 0
+#define KRSI_DTYPE_F16 1
+#define KRSI_DTYPE_F32 2
 
 enum krsi_status {
   KRSI_OK = 0,
@@ -33,7 +45,7 @@ enum krsi_status {
   KRSI_ERR_BAD_SHAPE = 2,       /* a size is <= 0 or out of the supported range */
   KRSI_ERR_MISALIGNED = 3,      /* a pointer or leading dimension breaks 16-byte alignment */
   KRSI_ERR_WORKSPACE = 4,       /* workspace missing or smaller than *_workspace_bytes() */
-  KRSI_ERR_UNSUPPORTED = 5,     /* a mode/dtype/head dim this build does not implement */
+  KRSI_ERR_UNSUPPORTED = 5,     /* a mode, dtype or head dim this build does not implement */
   KRSI_ERR_LAUNCH = 6,          /* the HIP runtime rejected a kernel launch */
   KRSI_ERR_BAD_SCALE = 7        /* scale or eps is not finite */
 };
@@ -44,51 +56,67 @@ const char* krsi_error_string(int status);
 /* ------------------------------------------------------------------ RMSNorm
  * Replaces library/rmsnorm.py:54-59 (_fwd: the _rms_fwd launch, :22-31).
  *   rstd[r] = 1 / sqrt(sum_c x[r,c]^2 / n + eps)            (fp32)
- *   y[r,c]  = bf16( w[c] * bf16(x[r,c] * rstd[r]) )
- * x, y: [rows, n] bf16 contiguous; w: [n] bf16; rstd: [rows] fp32.
+ *   y[r,c]  = T( w[c] * T(x[r,c] * rstd[r]) )                 T = dtype
+ * x, y: [rows, n] contiguous; w: [n]; all three of `dtype`; rstd: [rows] fp32.
  * Limits: 1 <= n <= 16384, rows >= 1 (rows == 0 is a no-op).        */
+int krsi_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
+                     int32_t n, float eps, int32_t dtype, void* stream);
 int krsi_rmsnorm_fwd_bf16(const void* x, const void* w, void* y, float* rstd,
                           int64_t rows, int32_t n, float eps, void* stream);
 
 /* Replaces library/rmsnorm.py:62-68 (_bwd: _rms_bwd :34-51 plus the torch
  * `dwp.sum(0).to(w.dtype)` reduction of the per-program partials).
- *   nrm   = bf16(x * rstd);  dn = float(bf16(g * w))
- *   dx    = rstd*dn - x*rstd^3 * sum_c(dn*x)/n                        (bf16 out)
- *   dw[c] = bf16( sum_r g[r,c] * nrm[r,c] )   fp32 accumulation, fixed order
+ *   nrm   = T(x * rstd);  dn = float(T(g * w))                       T = dtype
+ *   dx    = rstd*dn - x*rstd^3 * sum_c(dn*x)/n                        (T out)
+ *   dw[c] = T( sum_r g[r,c] * nrm[r,c] )      fp32 accumulation, fixed order
  * workspace: at least krsi_rmsnorm_bwd_workspace_bytes(rows, n) bytes of
- * device memory (fp32 per-block partials); its contents on entry are ignored. */
+ * device memory (fp32 per-block partials; the size is the same for every
+ * dtype); its contents on entry are ignored. */
 size_t krsi_rmsnorm_bwd_workspace_bytes(int64_t rows, int32_t n);
+int krsi_rmsnorm_bwd(const void* g, const void* x, const void* w, const float* rstd, void* dx,
+                     void* dw, void* workspace, size_t workspace_bytes, int64_t rows, int32_t n,
+                     int32_t dtype, void* stream);
 int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const float* rstd,
                           void* dx, void* dw, void* workspace, size_t workspace_bytes,
                           int64_t rows, int32_t n, void* stream);
 
 /* -------------------------------------------------------------------- GEGLU
  * Replaces library/geglu.py:55-61 (_fwd: _geglu_fwd :27-35).
- * u: [rows, 2f] bf16 contiguous, a = u[:, :f], b = u[:, f:]; out: [rows, f].
- *   out = bf16( bf16(gelu(a)) * b )
+ * u: [rows, 2f] contiguous, a = u[:, :f], b = u[:, f:]; out: [rows, f]; both of
+ * `dtype` (T):
+ *   out = T( T(gelu(a)) * b )
  * approximate: 1 = tanh form (the reference's only form, geglu.py:20-24),
  *              0 = exact erf form (torch.nn.functional.gelu default).      */
+int krsi_geglu_fwd(const void* u, void* out, int64_t rows, int32_t f, int32_t approximate,
+                   int32_t dtype, void* stream);
 int krsi_geglu_fwd_bf16(const void* u, void* out, int64_t rows, int32_t f,
                         int32_t approximate, void* stream);
 
 /* Replaces library/geglu.py:64-68 (_bwd: _geglu_bwd :38-52).
- * g: [rows, f] bf16; du: [rows, 2f] bf16 = [da | db]:
- *   db = bf16( g * bf16(gelu(a)) );  da = bf16( float(bf16(g*b)) * gelu'(a) ) */
+ * g: [rows, f]; du: [rows, 2f] = [da | db]; all of `dtype` (T):
+ *   db = T( g * T(gelu(a)) );  da = T( float(T(g*b)) * gelu'(a) )          */
+int krsi_geglu_bwd(const void* g, const void* u, void* du, int64_t rows, int32_t f,
+                   int32_t approximate, int32_t dtype, void* stream);
 int krsi_geglu_bwd_bf16(const void* g, const void* u, void* du, int64_t rows, int32_t f,
                         int32_t approximate, void* stream);
 
 /* ------------------------------------------------- relative-position attention
  * Replaces library/relpos_attention.py:132-140 (_forward: _fwd :26-59).
- * qkv: [B*S, ld_qkv] bf16, unit column stride; token t = b*S + s holds
+ * dtype: KRSI_DTYPE_BF16 or KRSI_DTYPE_F16 (T); P is rounded to T before the
+ * P V product, as the reference rounds it to v's dtype (:53).
+ * qkv: [B*S, ld_qkv] of T, unit column stride; token t = b*S + s holds
  *      q at columns [h*D, h*D+D), k at [H*D + h*D, ...), v at [2*H*D + h*D, ...).
  * pd:  [H, 2S-1] fp32, bias[h,i,j] = pd[h, j - i + S - 1].
- * out: [B*S, H*D] bf16; out32: same, fp32; lse: [B*H, S] fp32 in the log2
+ * out: [B*S, H*D] of T; out32: same, fp32; lse: [B*H, S] fp32 in the log2
  *      domain (lse = log2 sum_j 2^{(q.k*scale + bias) * log2(e)}).
  * Limits: D % 8 == 0 and 8 <= D <= 128, ld_qkv % 8 == 0, ld_qkv >= 3*H*D,
  *         S >= 1, S * ld_qkv * 2 < 2^31 bytes (UNSUPPORTED otherwise),
  *         scale finite, and scale == 0 or |scale| * log2(e) >= 2^-60
  *         (BAD_SCALE otherwise: the bias is folded into the score accumulator
  *         as pd * log2(e) / |scale * log2(e)|). Non-causal.                  */
+int krsi_relpos_fwd(const void* qkv, int64_t ld_qkv, const float* pd, void* out, float* out32,
+                    float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
+                    int32_t dtype, void* stream);
 int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void* out,
                          float* out32, float* lse, int32_t B, int32_t S, int32_t H,
                          int32_t D, float scale, void* stream);
@@ -97,10 +125,15 @@ int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void*
  * reduction, _bwd_dkdv :62-94, _bwd_dq :97-126 and the torch diagonal sum of
  * dbias into dpd). No [B,H,S,S] buffer: dpd is reduced in-kernel along the
  * diagonals j - i, into per-block partials summed in a fixed order.
- * dout: [B*S, H*D] bf16 contiguous; dqkv: [B*S, ld_dqkv] bf16 (same column
+ * dout: [B*S, H*D] of T contiguous; dqkv: [B*S, ld_dqkv] of T (same column
  * layout as qkv, every q/k/v column written); dpd: [H, 2S-1] fp32 (overwritten).
+ * P and dS are rounded to T before their products (:88-92, :125).
  * workspace: at least krsi_relpos_bwd_workspace_bytes(B,S,H,D) bytes.        */
 size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t D);
+int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
+                    const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv, float* dpd,
+                    void* workspace, size_t workspace_bytes, int32_t B, int32_t S, int32_t H,
+                    int32_t D, float scale, int32_t dtype, void* stream);
 int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
                          const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv,
                          float* dpd, void* workspace, size_t workspace_bytes, int32_t B,

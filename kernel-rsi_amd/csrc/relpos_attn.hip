@@ -1,5 +1,7 @@
 // Relative-position-bias flash attention (non-causal), forward and backward,
-// for gfx950 on bf16 MFMA (v_mfma_f32_32x32x16_bf16), fp32 softmax.
+// for gfx950 on 16-bit MFMA (v_mfma_f32_32x32x16_bf16 or _f16, by the activation
+// dtype DT), fp32 softmax. P and dS are rounded to DT before their products, as the
+// reference rounds them to the dtype of v and q.
 //
 // Semantics follow library/relpos_attention.py of the reference (kernel-rsi):
 //   s[i,j]   = (q_i . k_j * scale + pd[h, j - i + S - 1]) * log2(e)     (:46)
@@ -43,7 +45,8 @@
 //   * Online softmax keeps the exact running max per 64-key step (the step
 //     maximum gives p = 1, exact in bf16, as in the reference); the fp32
 //     accumulators are rescaled only when some lane's max moved. The row sum
-//     adds the bf16 p the PV product uses (v_dot2c_f32_bf16, two per op).
+//     adds the fp32 p (fp16) or the bf16 p the PV product uses (bf16:
+//     v_dot2c_f32_bf16, two per op).
 //   * dpd is reduced along the diagonals j - i inside the dK/dV kernel: each
 //     (wave, half-wave) adds its fp32 ds into private LDS rings indexed by
 //     diagonal, two diagonals per 64-bit read-modify-write. Within one
@@ -339,17 +342,25 @@ __device__ __forceinline__ int xcd_tile(int w, int N) {
   return x * q + min(x, r) + k;
 }
 
-// Row sum of bf16 p values: two per v_dot2c_f32_bf16 against (1, 1).
-__device__ __forceinline__ float add_bf16_pair(uint32_t pair, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
-                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+// The forward's row sum l: of the fp32 p, as the reference (relpos_attention.py:51), or of
+// the rounded p the P V product uses, two per v_dot2c_f32_bf16 / _f16 against (1, 1).
+template <int DT>
+constexpr bool kRowSumFp32 = (DT == kF16);
+template <int DT>
+__device__ __forceinline__ float add_pair(uint32_t pair, float acc) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, 0x3c003c00u),
+                                  acc, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
 }
 
 // ------------------------------------------------------------------- forward
 // One 64-key step of the forward for this lane's query: scores (bias folded into
 // the accumulator), exact running max, p = exp2(acc c - m), l += bf16(p),
 // O^T += V^T P^T. TAIL masks keys >= S (last step only).
-template <int DP, int NW, bool TAIL>
+template <int DT, int DP, int NW, bool TAIL>
 __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
                                          const TileLane<DP>& L, const u32x4* qreg, f32x16* oacc,
                                          float& m_run, float* l_run, int j0, int S, int ii, int g,
@@ -361,7 +372,7 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
   for (int kb = 0; kb < 2; ++kb) {
     sc[kb] = read_bias16<NW>(Bw, kb * 32 + 4 * g + (K::ROWS - 1) - ii);
 #pragma unroll
-    for (int s = 0; s < G::KS; ++s) sc[kb] = mfma32x32x16(row_operand<DP>(Ks, L, kb * 32, s), qreg[s], sc[kb]);
+    for (int s = 0; s < G::KS; ++s) sc[kb] = mfma32x32x16<DT>(row_operand<DP>(Ks, L, kb * 32, s), qreg[s], sc[kb]);
   }
   if (TAIL) {
 #pragma unroll
@@ -399,19 +410,24 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
     for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][r], c, negm));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const u32x4 pb = pack8(&p[8 * u]);
+      const u32x4 pb = Elem<DT>::pack(&p[8 * u]);
+      if constexpr (kRowSumFp32<DT>) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) l_run[w & 1] = add_bf16_pair(pb[w], l_run[w & 1]);
+        for (int w = 0; w < 8; ++w) l_run[w & 1] += p[8 * u + w];
+      } else {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) l_run[w & 1] = add_pair<DT>(pb[w], l_run[w & 1]);
+      }
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
-        oacc[db] = mfma32x32x16(tr_operand<DP>(Vs, L, 2 * kb + u, db), pb, oacc[db]);
+        oacc[db] = mfma32x32x16<DT>(tr_operand<DP>(Vs, L, 2 * kb + u, db), pb, oacc[db]);
     }
   }
 }
 
-// O = acc / l stored as fp32 and bf16 (head-dim columns 32db + 8a + 4g ..+3 of this lane's
-// query), lse = m + log2 l.
-template <int DP>
+// O = acc / l stored as fp32 and in the activation dtype (head-dim columns 32db + 8a + 4g
+// ..+3 of this lane's query), lse = m + log2 l.
+template <int DT, int DP>
 __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const float* l_run,
                                           bool qvalid, int g, int64_t obase, int D,
                                           uint16_t* __restrict__ out, float* __restrict__ out32,
@@ -429,8 +445,8 @@ __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const
         for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
         *reinterpret_cast<f32x4*>(out32 + obase + d0) = o;
         uint2 ob;
-        ob.x = pack_bf16x2(o[0], o[1]);
-        ob.y = pack_bf16x2(o[2], o[3]);
+        ob.x = Elem<DT>::pack2(o[0], o[1]);
+        ob.y = Elem<DT>::pack2(o[2], o[3]);
         *reinterpret_cast<uint2*>(out + obase + d0) = ob;
       }
     }
@@ -440,7 +456,7 @@ __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const
 // At head dims 49-64 (DP = 64) the forward runs 4 waves per SIMD (128 VGPRs; spills only in the
 // prologue and the last step): more waves give one wave's VALU softmax more MFMA work of the
 // others to overlap with (-2% at config 5 against 3 waves).
-template <int DP, int NW>
+template <int DT, int DP, int NW>
 __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
@@ -510,7 +526,7 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
       dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
       load_bias<NW>(bst, pdh, npd, wb0 + j1, 1);
     }
-    fwd_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, oacc,
+    fwd_step<DT, DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, oacc,
                                             m_run, l_run, t * kStep, S, ii, g, c);
   };
   // Full 64-key steps carry no key mask; a partial last step (S % 64 != 0) runs once after
@@ -529,7 +545,7 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
       step(t, kBuf0, kTail);
   }
 
-  fwd_store<DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
+  fwd_store<DT, DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
                 lse + (int64_t)bh * S + qi);
 }
 
@@ -537,7 +553,7 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
 // One 64-key step of the dQ kernel for this lane's query: p = exp2(acc c - lse),
 // ds = p (dp - delta), dQ^T += K^T dS^T. Invalid query lanes carry lse = +inf, so
 // their p is 0 without a mask; TAIL masks keys >= S (last step only).
-template <int DP, int NW, bool TAIL>
+template <int DT, int DP, int NW, bool TAIL>
 __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
                                         const TileLane<DP>& L, const u32x4* qreg, const u32x4* doreg,
                                         f32x16* dq, float neg_lse, float delta, int j0, int S, int ii,
@@ -552,8 +568,8 @@ __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, 
     for (int r = 0; r < 16; ++r) accp[r] = 0.f;
 #pragma unroll
     for (int s = 0; s < G::KS; ++s) {
-      acc = mfma32x32x16(row_operand<DP>(Ks, L, kb * 32, s), qreg[s], acc);
-      accp = mfma32x32x16(row_operand<DP>(Vs, L, kb * 32, s), doreg[s], accp);
+      acc = mfma32x32x16<DT>(row_operand<DP>(Ks, L, kb * 32, s), qreg[s], acc);
+      accp = mfma32x32x16<DT>(row_operand<DP>(Vs, L, kb * 32, s), doreg[s], accp);
     }
     float ds[16];
 #pragma unroll
@@ -564,15 +580,15 @@ __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, 
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const u32x4 dsb = pack8(&ds[8 * u]);
+      const u32x4 dsb = Elem<DT>::pack(&ds[8 * u]);
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
-        dq[db] = mfma32x32x16(tr_operand<DP>(Ks, L, 2 * kb + u, db), dsb, dq[db]);
+        dq[db] = mfma32x32x16<DT>(tr_operand<DP>(Ks, L, 2 * kb + u, db), dsb, dq[db]);
     }
   }
 }
 
-template <int DP, int NW>
+template <int DT, int DP, int NW>
 __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ out32,
@@ -621,7 +637,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
       const f32x4 o0 = *reinterpret_cast<const f32x4*>(out32 + obase + d0);
       const f32x4 o1 = *reinterpret_cast<const f32x4*>(out32 + obase + d0 + 4);
       float df[8];
-      unpack8(doreg[s], df);
+      Elem<DT>::unpack(doreg[s], df);
 #pragma unroll
       for (int e = 0; e < 4; ++e) dsum += df[e] * o0[e];
 #pragma unroll
@@ -660,7 +676,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
       dma_tile<DP, K::NT>(Vs + (1 - B) * TILE, voff, v0p, ld, j1, S, D);
       load_bias<NW>(bst, pdh, npd, wb0 + j1, 1);
     }
-    dq_step<DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, doreg,
+    dq_step<DT, DP, NW, decltype(tail)::value>(Ks + B * TILE, Vs + B * TILE, Bw + B * BWIN, L, qreg, doreg,
                                            dq, neg_lse, delta, t * kStep, S, ii, g, c);
   };
   // Full 64-key steps carry no key mask; a partial last step runs once after the loop.
@@ -687,8 +703,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
         const int d0 = db * 32 + 8 * a + 4 * g;
         if (d0 < D) {
           uint2 ob;
-          ob.x = pack_bf16x2(dq[db][4 * a] * scale, dq[db][4 * a + 1] * scale);
-          ob.y = pack_bf16x2(dq[db][4 * a + 2] * scale, dq[db][4 * a + 3] * scale);
+          ob.x = Elem<DT>::pack2(dq[db][4 * a] * scale, dq[db][4 * a + 1] * scale);
+          ob.y = Elem<DT>::pack2(dq[db][4 * a + 2] * scale, dq[db][4 * a + 3] * scale);
           *reinterpret_cast<uint2*>(dqkv + qbase + d0) = ob;
         }
       }
@@ -752,7 +768,7 @@ __device__ __forceinline__ float ring_fold(float* ring, int r, int off1) {
   for (int e = 0; e < 8; ++e) v += x[e];
   return quad_sum(v);
 }
-template <int DP, int NW>
+template <int DT, int DP, int NW>
 __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
@@ -874,8 +890,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       }
 #pragma unroll
       for (int s = 0; s < G::KS; ++s) {
-        acc = mfma32x32x16(row_operand<DP>(Qb, L, qb * 32, s), kreg[s], acc);
-        accp = mfma32x32x16(row_operand<DP>(Ob, L, qb * 32, s), vreg[s], accp);
+        acc = mfma32x32x16<DT>(row_operand<DP>(Qb, L, qb * 32, s), kreg[s], acc);
+        accp = mfma32x32x16<DT>(row_operand<DP>(Ob, L, qb * 32, s), vreg[s], accp);
       }
       float p[16], ds[16];
 #pragma unroll
@@ -905,12 +921,12 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
         }
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const u32x4 pa = pack8(&p[8 * u]);
-        const u32x4 dsa = pack8(&ds[8 * u]);
+        const u32x4 pa = Elem<DT>::pack(&p[8 * u]);
+        const u32x4 dsa = Elem<DT>::pack(&ds[8 * u]);
 #pragma unroll
         for (int db = 0; db < G::DB; ++db) {
-          dv[db] = mfma32x32x16(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
-          dk[db] = mfma32x32x16(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
+          dv[db] = mfma32x32x16<DT>(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
+          dk[db] = mfma32x32x16<DT>(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
         }
       }
       // Diagonals [S + 63 - 64(t-1), S + 126 - 64(t-1)] got their last ds in step t-1 (step
@@ -954,8 +970,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
         const int key = j_wg + wave * 32 + kperm(8 * (r >> 2) + 4 * g + (r & 3));
         if (key < S) {
           uint16_t* rowp = dqkv + (tok0 + key) * ldd + HD + (int64_t)h * D + d;
-          rowp[0] = f32_to_bf16(dk[db][r] * scale);
-          rowp[HD] = f32_to_bf16(dv[db][r]);
+          rowp[0] = Elem<DT>::store(dk[db][r] * scale);
+          rowp[HD] = Elem<DT>::store(dv[db][r]);
         }
       }
     }
@@ -1005,7 +1021,7 @@ int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float sc
   if (D % 8 != 0 || D > 128) return KRSI_ERR_UNSUPPORTED;
   if ((int64_t)B * H > 65535 || S > (1 << 24)) return KRSI_ERR_BAD_SHAPE;
   if (ld < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
-  // Buffer resources of one (batch, head) slice hold S rows of ld bf16 in < 2^31 bytes.
+  // Buffer resources of one (batch, head) slice hold S rows of ld 16-bit values in < 2^31 bytes.
   if ((int64_t)S * ld * 2 >= ((int64_t)1 << 31)) return KRSI_ERR_UNSUPPORTED;
   if (ld % 8 != 0 || !aligned16(qkv)) return KRSI_ERR_MISALIGNED;
   if (!(scale == scale) || scale > 3.0e38f || scale < -3.0e38f) return KRSI_ERR_BAD_SCALE;
@@ -1032,16 +1048,16 @@ size_t ws_part_bytes(int B, int S, int H) {
   return align256((size_t)B * H * nkb * (size_t)(S + kKvRows) * sizeof(float));
 }
 
-template <int DP>
+template <int DT, int DP>
 void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* out32, float* lse,
                 int B, int S, int H, int D, Fold f, hipStream_t st) {
   using K = Blk<kFwdNW>;
   const dim3 grid((unsigned)(ceil_div(S, K::ROWS) * B * H));
-  hipLaunchKernelGGL((relpos_fwd_kernel<DP, kFwdNW>), grid, dim3(K::NT), 0, st,
+  hipLaunchKernelGGL((relpos_fwd_kernel<DT, DP, kFwdNW>), grid, dim3(K::NT), 0, st,
                      (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
 }
 
-template <int DP>
+template <int DT, int DP>
 void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
                 const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S, int H,
                 int D, Fold f, float scale, hipStream_t st) {
@@ -1051,10 +1067,10 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_delta_bytes(B, S, H));
   const int nqb = (int)ceil_div(S, KQ::ROWS);
   const int nkb = (int)ceil_div(S, KK::ROWS);
-  hipLaunchKernelGGL((relpos_bwd_dq_kernel<DP, kDqNW>), dim3((unsigned)(nqb * B * H)),
+  hipLaunchKernelGGL((relpos_bwd_dq_kernel<DT, DP, kDqNW>), dim3((unsigned)(nqb * B * H)),
                      dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
                      lse, delta, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
-  hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DP, kDkdvNW>), dim3((unsigned)(nkb * B * H)),
+  hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DT, DP, kDkdvNW>), dim3((unsigned)(nkb * B * H)),
                      dim3(KK::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
                      (const float*)delta, (uint16_t*)dqkv, ldd, part, S, H, D, f, scale);
   const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
@@ -1062,25 +1078,13 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
                      nkb, KK::ROWS);
 }
 
-}  // namespace
-}  // namespace krsi
-
-extern "C" {
-
-int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void* out, float* out32,
-                         float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
-                         void* stream) {
-  using namespace krsi;
-  if (!qkv || !pd || !out || !out32 || !lse) return KRSI_ERR_NULL_POINTER;
-  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
-  if (rc != KRSI_OK) return rc;
-  if (!aligned16(out) || !aligned16(out32)) return KRSI_ERR_MISALIGNED;
-  const Fold f = fold_scale(scale);
-  hipStream_t st = as_stream(stream);
+template <int DT>
+int dispatch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* out32, float* lse,
+                 int B, int S, int H, int D, Fold f, hipStream_t st) {
   switch (padded_dim(D)) {
 #define KRSI_CASE(DPV_)                                                                \
   case DPV_:                                                                           \
-    launch_fwd<DPV_>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, f, st);             \
+    launch_fwd<DT, DPV_>(qkv, ld, pd, out, out32, lse, B, S, H, D, f, st);             \
     break;
     KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
     KRSI_CASE(112) KRSI_CASE(128)
@@ -1091,6 +1095,52 @@ int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void*
   return launch_status();
 }
 
+template <int DT>
+int dispatch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
+                 const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S,
+                 int H, int D, Fold f, float scale, hipStream_t st) {
+  switch (padded_dim(D)) {
+#define KRSI_CASE(DPV_)                                                                          \
+  case DPV_:                                                                                     \
+    launch_bwd<DT, DPV_>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, dpd, ws, B, S, H, D, f, scale, \
+                         st);                                                                    \
+    break;
+    KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
+    KRSI_CASE(112) KRSI_CASE(128)
+#undef KRSI_CASE
+    default:
+      return KRSI_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace krsi
+
+extern "C" {
+
+int krsi_relpos_fwd(const void* qkv, int64_t ld_qkv, const float* pd, void* out, float* out32,
+                    float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
+                    int32_t dtype, void* stream) {
+  using namespace krsi;
+  if (dtype != kBf16 && dtype != kF16) return KRSI_ERR_UNSUPPORTED;
+  if (!qkv || !pd || !out || !out32 || !lse) return KRSI_ERR_NULL_POINTER;
+  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
+  if (rc != KRSI_OK) return rc;
+  if (!aligned16(out) || !aligned16(out32)) return KRSI_ERR_MISALIGNED;
+  const Fold f = fold_scale(scale);
+  hipStream_t st = as_stream(stream);
+  return dtype == kF16 ? dispatch_fwd<kF16>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, f, st)
+                       : dispatch_fwd<kBf16>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, f, st);
+}
+
+int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void* out, float* out32,
+                         float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
+                         void* stream) {
+  return krsi_relpos_fwd(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, scale, KRSI_DTYPE_BF16,
+                         stream);
+}
+
 size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t D) {
   using namespace krsi;
   (void)D;
@@ -1098,11 +1148,12 @@ size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t 
   return ws_delta_bytes(B, S, H) + ws_part_bytes(B, S, H);
 }
 
-int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
-                         const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv,
-                         float* dpd, void* workspace, size_t workspace_bytes, int32_t B, int32_t S,
-                         int32_t H, int32_t D, float scale, void* stream) {
+int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
+                    const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv, float* dpd,
+                    void* workspace, size_t workspace_bytes, int32_t B, int32_t S, int32_t H,
+                    int32_t D, float scale, int32_t dtype, void* stream) {
   using namespace krsi;
+  if (dtype != kBf16 && dtype != kF16) return KRSI_ERR_UNSUPPORTED;
   if (!dout || !qkv || !pd || !out32 || !lse || !dqkv || !dpd) return KRSI_ERR_NULL_POINTER;
   int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
   if (rc != KRSI_OK) return rc;
@@ -1114,19 +1165,19 @@ int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, cons
   if (!aligned16(workspace)) return KRSI_ERR_MISALIGNED;
   const Fold f = fold_scale(scale);
   hipStream_t st = as_stream(stream);
-  switch (padded_dim(D)) {
-#define KRSI_CASE(DPV_)                                                                      \
-  case DPV_:                                                                                 \
-    launch_bwd<DPV_>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace, B, S, \
-                     H, D, f, scale, st);                                                    \
-    break;
-    KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
-    KRSI_CASE(112) KRSI_CASE(128)
-#undef KRSI_CASE
-    default:
-      return KRSI_ERR_UNSUPPORTED;
-  }
-  return launch_status();
+  return dtype == kF16
+             ? dispatch_bwd<kF16>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace,
+                                  B, S, H, D, f, scale, st)
+             : dispatch_bwd<kBf16>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace,
+                                   B, S, H, D, f, scale, st);
+}
+
+int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
+                         const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv,
+                         float* dpd, void* workspace, size_t workspace_bytes, int32_t B, int32_t S,
+                         int32_t H, int32_t D, float scale, void* stream) {
+  return krsi_relpos_bwd(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace,
+                         workspace_bytes, B, S, H, D, scale, KRSI_DTYPE_BF16, stream);
 }
 
 }  // extern "C"

@@ -3,17 +3,19 @@
 // Semantics follow library/rmsnorm.py of the reference (kernel-rsi):
 //   forward  (_rms_fwd, rmsnorm.py:22-31):
 //     rstd = 1 / sqrt(sum(x^2) / N + eps)            fp32, stored per row
-//     y    = w * bf16(x * rstd)                      (bf16 x bf16 -> bf16)
+//     y    = w * T(x * rstd)                         (T x T -> T)
 //   backward (_rms_bwd, rmsnorm.py:34-51, and the dwp.sum(0) of :68):
-//     nrm  = bf16(x * rstd)
+//     nrm  = T(x * rstd)
 //     dw  += g * nrm                                 fp32, per block, then a
 //                                                    fixed-order column sum
-//     dn   = float(bf16(g * w))
+//     dn   = float(T(g * w))
 //     dx   = rstd * dn - x * rstd^3 * (sum(dn * x) / N)
+//   T is the activation dtype (bf16, fp16 or fp32: the template parameter DT),
+//   as the reference rounds to w's dtype; T(.) is round-to-nearest-even.
 //
 // Design (MI355X): each row is owned by one wavefront (WPR = 1, N <= 4096) or
 // by WPR wavefronts of one workgroup (N <= 8192 / 16384). Every lane moves
-// whole 16-byte chunks of 8 bf16, so a wave reads 1 KiB per instruction
+// whole 16-byte chunks (8 bf16 / fp16 or 4 fp32), so a wave reads 1 KiB per instruction
 // and the row lives in registers between the reduction and the write. The
 // backward is persistent: a fixed grid of NB workgroups walks the rows, keeps
 // its share of dw in fp32 registers and writes one partial row per workgroup;
@@ -30,18 +32,19 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
-constexpr int kMaxChunksPerLane = 8;   // 8 x 8 bf16 = 64 elements per lane
 constexpr int kBwdMaxBlocks = 512;     // persistent grid of the backward
 constexpr int kColsumRows = 32;        // partial rows folded per first-level column-sum block
 constexpr int kScalarRowChunk = 64;    // rows per block of the scalar dw kernel
 
 // ----------------------------------------------------------------- forward
-template <int WPR, int VPT>
-__global__ __launch_bounds__(kThreads) void rms_fwd_vec(const uint16_t* __restrict__ x,
-                                                        const uint16_t* __restrict__ w,
-                                                        uint16_t* __restrict__ y,
+template <int DT, int WPR, int VPT>
+__global__ __launch_bounds__(kThreads) void rms_fwd_vec(const typename Elem<DT>::T* __restrict__ x,
+                                                        const typename Elem<DT>::T* __restrict__ w,
+                                                        typename Elem<DT>::T* __restrict__ y,
                                                         float* __restrict__ rstd, int64_t rows,
                                                         int n, float eps) {
+  using El = Elem<DT>;
+  constexpr int E = El::E;                   // elements per 16-byte chunk
   constexpr int RPB = kWavesPerBlock / WPR;  // rows per block
   constexpr int GT = WPR * kWave;            // threads per row group
   __shared__ float red[kWavesPerBlock];
@@ -50,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const uint16_t* __restri
   const int gtid = threadIdx.x - grp * GT;
   const int64_t row = (int64_t)blockIdx.x * RPB + grp;
   const bool live = row < rows;
-  const int nch = n >> 3;
+  const int nch = n / E;
 
   u32x4 xv[VPT];
   float ss = 0.f;
@@ -62,10 +65,10 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const uint16_t* __restri
   }
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
-    float f[8];
-    unpack8(xv[k], f);
+    float f[E];
+    El::unpack(xv[k], f);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    for (int j = 0; j < E; ++j) ss += f[j] * f[j];
   }
   ss = wave_sum(ss);
   if (WPR > 1) {
@@ -84,48 +87,52 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const uint16_t* __restri
   for (int k = 0; k < VPT; ++k) {
     const int c = gtid + k * GT;
     if (c < nch) {
-      float xf[8], wf[8], o[8];
-      unpack8(xv[k], xf);
-      unpack8(wr[c], wf);
+      float xf[E], wf[E], o[E];
+      El::unpack(xv[k], xf);
+      El::unpack(wr[c], wf);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = wf[j] * round_bf16(xf[j] * r);
-      __builtin_nontemporal_store(pack8(o), &yr[c]);  // streamed out, not re-read
+      for (int j = 0; j < E; ++j) o[j] = wf[j] * El::round(xf[j] * r);
+      __builtin_nontemporal_store(El::pack(o), &yr[c]);  // streamed out, not re-read
     }
   }
 }
 
 // One wave per row, any alignment, any n.
-__global__ __launch_bounds__(kThreads) void rms_fwd_scalar(const uint16_t* __restrict__ x,
-                                                           const uint16_t* __restrict__ w,
-                                                           uint16_t* __restrict__ y,
+template <int DT>
+__global__ __launch_bounds__(kThreads) void rms_fwd_scalar(const typename Elem<DT>::T* __restrict__ x,
+                                                           const typename Elem<DT>::T* __restrict__ w,
+                                                           typename Elem<DT>::T* __restrict__ y,
                                                            float* __restrict__ rstd, int64_t rows,
                                                            int n, float eps) {
+  using El = Elem<DT>;
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
   if (row >= rows) return;
-  const uint16_t* xr = x + row * (int64_t)n;
+  const typename El::T* xr = x + row * (int64_t)n;
   float ss = 0.f;
   for (int c = lane; c < n; c += kWave) {
-    const float f = bf16_to_f32(xr[c]);
+    const float f = El::load(xr[c]);
     ss += f * f;
   }
   ss = wave_sum(ss);
   const float r = 1.0f / __fsqrt_rn(ss / (float)n + eps);
   if (lane == 0) rstd[row] = r;
-  uint16_t* yr = y + row * (int64_t)n;
+  typename El::T* yr = y + row * (int64_t)n;
   for (int c = lane; c < n; c += kWave)
-    yr[c] = f32_to_bf16(bf16_to_f32(w[c]) * round_bf16(bf16_to_f32(xr[c]) * r));
+    yr[c] = El::store(El::load(w[c]) * El::round(El::load(xr[c]) * r));
 }
 
 // ---------------------------------------------------------------- backward
 // Persistent: gridDim.x blocks, each block handles row groups
 // blockIdx.x, blockIdx.x + gridDim.x, ... Every group of the block runs the
 // same number of iterations so that the WPR > 1 barriers stay uniform.
-template <int WPR, int VPT>
+template <int DT, int WPR, int VPT>
 __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
-    const uint16_t* __restrict__ g, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const float* __restrict__ rstd, uint16_t* __restrict__ dx, float* __restrict__ part,
-    int64_t rows, int n) {
+    const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
+    const typename Elem<DT>::T* __restrict__ w, const float* __restrict__ rstd,
+    typename Elem<DT>::T* __restrict__ dx, float* __restrict__ part, int64_t rows, int n) {
+  using El = Elem<DT>;
+  constexpr int E = El::E;
   constexpr int RPB = kWavesPerBlock / WPR;
   constexpr int GT = WPR * kWave;
   __shared__ float red[2][kWavesPerBlock];
@@ -133,18 +140,18 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
   const int wave = threadIdx.x / kWave;
   const int grp = wave / WPR;
   const int gtid = threadIdx.x - grp * GT;
-  const int nch = n >> 3;
+  const int nch = n / E;
   const float inv_n = 1.0f / (float)n;
 
-  float wv[VPT][8];
-  float dw[VPT][8];
+  float wv[VPT][E];
+  float dw[VPT][E];
   const u32x4* wr = reinterpret_cast<const u32x4*>(w);
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     const int c = gtid + k * GT;
-    unpack8(c < nch ? wr[c] : u32x4{0u, 0u, 0u, 0u}, wv[k]);
+    El::unpack(c < nch ? wr[c] : u32x4{0u, 0u, 0u, 0u}, wv[k]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dw[k][j] = 0.f;
+    for (int j = 0; j < E; ++j) dw[k][j] = 0.f;
   }
 
   const int64_t groups_total = (int64_t)gridDim.x * RPB;
@@ -179,14 +186,14 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
     float sdot = 0.f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-      float gf[8], xf[8];
-      unpack8(gv[k], gf);
-      unpack8(xv[k], xf);
+      float gf[E], xf[E];
+      El::unpack(gv[k], gf);
+      El::unpack(xv[k], xf);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float nrm = round_bf16(xf[j] * r);
+      for (int j = 0; j < E; ++j) {
+        const float nrm = El::round(xf[j] * r);
         dw[k][j] += gf[j] * nrm;
-        const float dn = round_bf16(gf[j] * wv[k][j]);
+        const float dn = El::round(gf[j] * wv[k][j]);
         sdot += dn * xf[j];
       }
     }
@@ -206,15 +213,15 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
       for (int k = 0; k < VPT; ++k) {
         const int c = gtid + k * GT;
         if (c < nch) {
-          float gf[8], xf[8], o[8];
-          unpack8(gv[k], gf);
-          unpack8(xv[k], xf);
+          float gf[E], xf[E], o[E];
+          El::unpack(gv[k], gf);
+          El::unpack(xv[k], xf);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float dn = round_bf16(gf[j] * wv[k][j]);
+          for (int j = 0; j < E; ++j) {
+            const float dn = El::round(gf[j] * wv[k][j]);
             o[j] = r * dn - (xf[j] * r3) * sn;
           }
-          __builtin_nontemporal_store(pack8(o), &dxr[c]);
+          __builtin_nontemporal_store(El::pack(o), &dxr[c]);
         }
       }
     }
@@ -230,28 +237,25 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
 
   // Fold the RPB row groups' dw into one partial row per block, in group
   // order, through a 4096-float LDS window.
+  constexpr int WCH = 4096 / E;  // chunks per LDS window
   float* prow = part + (int64_t)blockIdx.x * n;
-  for (int w0 = 0; w0 < nch; w0 += 512) {
+  for (int w0 = 0; w0 < nch; w0 += WCH) {
     for (int gi = 0; gi < RPB; ++gi) {
       if (grp == gi) {
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
           const int c = gtid + k * GT;
-          if (c >= w0 && c < w0 + 512 && c < nch) {
-            f32x4* cw = reinterpret_cast<f32x4*>(comb + (c - w0) * 8);
-            f32x4 lo{dw[k][0], dw[k][1], dw[k][2], dw[k][3]};
-            f32x4 hi{dw[k][4], dw[k][5], dw[k][6], dw[k][7]};
-            if (gi > 0) {
-              lo = cw[0] + lo;
-              hi = cw[1] + hi;
-            }
-            if (gi == RPB - 1) {
-              f32x4* pw = reinterpret_cast<f32x4*>(prow + c * 8);
-              pw[0] = lo;
-              pw[1] = hi;
-            } else {
-              cw[0] = lo;
-              cw[1] = hi;
+          if (c >= w0 && c < w0 + WCH && c < nch) {
+            f32x4* cw = reinterpret_cast<f32x4*>(comb + (c - w0) * E);
+            f32x4* pw = reinterpret_cast<f32x4*>(prow + c * E);
+#pragma unroll
+            for (int q = 0; q < E / 4; ++q) {
+              f32x4 v{dw[k][4 * q], dw[k][4 * q + 1], dw[k][4 * q + 2], dw[k][4 * q + 3]};
+              if (gi > 0) v = cw[q] + v;
+              if (gi == RPB - 1)
+                pw[q] = v;
+              else
+                cw[q] = v;
             }
           }
         }
@@ -262,9 +266,12 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
 }
 
 // Scalar backward, dx only (one wave per row, two passes over the row).
+template <int DT>
 __global__ __launch_bounds__(kThreads) void rms_bwd_dx_scalar(
-    const uint16_t* __restrict__ g, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const float* __restrict__ rstd, uint16_t* __restrict__ dx, int64_t rows, int n) {
+    const typename Elem<DT>::T* __restrict__ g, const typename Elem<DT>::T* __restrict__ x,
+    const typename Elem<DT>::T* __restrict__ w, const float* __restrict__ rstd,
+    typename Elem<DT>::T* __restrict__ dx, int64_t rows, int n) {
+  using El = Elem<DT>;
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
   if (row >= rows) return;
@@ -272,22 +279,23 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_dx_scalar(
   const float r = rstd[row];
   float sdot = 0.f;
   for (int c = lane; c < n; c += kWave) {
-    const float dn = round_bf16(bf16_to_f32(g[base + c]) * bf16_to_f32(w[c]));
-    sdot += dn * bf16_to_f32(x[base + c]);
+    const float dn = El::round(El::load(g[base + c]) * El::load(w[c]));
+    sdot += dn * El::load(x[base + c]);
   }
   sdot = wave_sum(sdot);
   const float r3 = r * r * r;
   const float sn = sdot * (1.0f / (float)n);
   for (int c = lane; c < n; c += kWave) {
-    const float xf = bf16_to_f32(x[base + c]);
-    const float dn = round_bf16(bf16_to_f32(g[base + c]) * bf16_to_f32(w[c]));
-    dx[base + c] = f32_to_bf16(r * dn - (xf * r3) * sn);
+    const float xf = El::load(x[base + c]);
+    const float dn = El::round(El::load(g[base + c]) * El::load(w[c]));
+    dx[base + c] = El::store(r * dn - (xf * r3) * sn);
   }
 }
 
 // Scalar dw partials: block (column tile, row chunk) -> part[row chunk][col].
-__global__ __launch_bounds__(kThreads) void rms_bwd_dw_scalar(const uint16_t* __restrict__ g,
-                                                              const uint16_t* __restrict__ x,
+template <int DT>
+__global__ __launch_bounds__(kThreads) void rms_bwd_dw_scalar(const typename Elem<DT>::T* __restrict__ g,
+                                                              const typename Elem<DT>::T* __restrict__ x,
                                                               const float* __restrict__ rstd,
                                                               float* __restrict__ part,
                                                               int64_t rows, int n, int64_t chunk) {
@@ -298,20 +306,20 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_dw_scalar(const uint16_t* __
   float acc = 0.f;
   for (int64_t r = r0; r < r1; ++r) {
     const int64_t i = r * n + col;
-    acc += bf16_to_f32(g[i]) * round_bf16(bf16_to_f32(x[i]) * rstd[r]);
+    acc += Elem<DT>::load(g[i]) * Elem<DT>::round(Elem<DT>::load(x[i]) * rstd[r]);
   }
   part[(int64_t)blockIdx.y * n + col] = acc;
 }
 
 // Column sums of a [R, n] fp32 matrix in fixed order. Block (64 columns, row
 // group of `rpg` rows): lane = column, the 4 waves take every 4th row of the
-// group, then the 4 wave sums are added in wave order. FINAL writes bf16,
+// group, then the 4 wave sums are added in wave order. FINAL writes dtype DT,
 // else one fp32 row per row group for the next level. Many small blocks keep
 // enough loads in flight to stream the partials at HBM rate.
-template <bool FINAL>
+template <bool FINAL, int DT = kBf16>
 __global__ __launch_bounds__(kThreads) void colsum(const float* __restrict__ in, int64_t R, int n,
                                                    int64_t rpg, float* __restrict__ outf,
-                                                   uint16_t* __restrict__ outb) {
+                                                   typename Elem<DT>::T* __restrict__ outb) {
   __shared__ float s[kWavesPerBlock][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -328,55 +336,56 @@ __global__ __launch_bounds__(kThreads) void colsum(const float* __restrict__ in,
   if (wave == 0 && col < n) {
     const float t = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
     if (FINAL)
-      outb[col] = f32_to_bf16(t);
+      outb[col] = Elem<DT>::store(t);
     else
       outf[(int64_t)blockIdx.y * n + col] = t;
   }
 }
 
-bool vec_ok(int n, std::initializer_list<const void*> ptrs) {
-  if (n % 8 != 0) return false;
+bool vec_ok(int n, int e, std::initializer_list<const void*> ptrs) {
+  if (n % e != 0) return false;
   for (const void* p : ptrs)
     if (!aligned16(p)) return false;
   return true;
 }
 
-template <int WPR, int VPT>
+template <int DT, int WPR, int VPT>
 void launch_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows, int n, float eps,
                 hipStream_t st) {
+  using T = typename Elem<DT>::T;
   constexpr int RPB = kWavesPerBlock / WPR;
   const int64_t blocks = ceil_div(rows, RPB);
-  hipLaunchKernelGGL((rms_fwd_vec<WPR, VPT>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
-                     (const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, rstd, rows, n, eps);
+  hipLaunchKernelGGL((rms_fwd_vec<DT, WPR, VPT>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
+                     (const T*)x, (const T*)w, (T*)y, rstd, rows, n, eps);
 }
 
-template <int WPR, int VPT>
+template <int DT, int WPR, int VPT>
 int64_t launch_bwd(const void* g, const void* x, const void* w, const float* rstd, void* dx,
                    float* part, int64_t rows, int n, hipStream_t st) {
+  using T = typename Elem<DT>::T;
   constexpr int RPB = kWavesPerBlock / WPR;
   int64_t blocks = ceil_div(rows, RPB);
   if (blocks > kBwdMaxBlocks) blocks = kBwdMaxBlocks;
-  hipLaunchKernelGGL((rms_bwd_vec<WPR, VPT>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
-                     (const uint16_t*)g, (const uint16_t*)x, (const uint16_t*)w, rstd,
-                     (uint16_t*)dx, part, rows, n);
+  hipLaunchKernelGGL((rms_bwd_vec<DT, WPR, VPT>), dim3((unsigned)blocks), dim3(kThreads), 0, st,
+                     (const T*)g, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows, n);
   return blocks;
 }
 
-// Chunks of 8 per lane for a row of n bf16 split over WPR waves, rounded up
-// to the next instantiated count.
-int pick_vpt(int n, int wpr) {
-  const int need = (int)ceil_div(n / 8, (int64_t)wpr * kWave);
+// 16-byte chunks per lane for a row of nch chunks split over WPR waves, rounded
+// up to a power of two (the instantiated counts).
+int pick_vpt(int nch, int wpr) {
+  const int need = (int)ceil_div(nch, (int64_t)wpr * kWave);
   int v = 1;
   while (v < need) v <<= 1;
   return v;
 }
 
-// Rows wider than 2048 take a whole workgroup (4 waves): fewer registers per
-// lane, more waves in flight.
-int pick_wpr(int n) { return n <= 2048 ? 1 : 4; }
+// Rows wider than 256 chunks (4 KiB) take a whole workgroup (4 waves): fewer
+// registers per lane, more waves in flight.
+int pick_wpr(int nch) { return nch <= 256 ? 1 : 4; }
 // The backward holds w, its dw share and two rows of g and x per lane, so it
-// spreads a row over more waves: at most 2 chunks per lane up to n = 4096.
-int pick_wpr_bwd(int n) { return n <= 1024 ? 1 : (n <= 2048 ? 2 : 4); }
+// spreads a row over more waves: at most 2 chunks per lane up to 512 chunks.
+int pick_wpr_bwd(int nch) { return nch <= 128 ? 1 : (nch <= 256 ? 2 : 4); }
 
 // Rows per block of the scalar dw kernel: at least kScalarRowChunk, and few
 // enough blocks that the partials stay within kBwdMaxBlocks rows.
@@ -385,20 +394,106 @@ int64_t scalar_chunk(int64_t rows) {
   return c > kScalarRowChunk ? c : kScalarRowChunk;
 }
 
-// Rows of partials the backward writes before the column sums (<= 512).
-int64_t bwd_partial_rows(int64_t rows, int n, bool vec) {
+// Rows of partials the backward writes before the column sums (<= 512), for
+// elements of e per chunk.
+int64_t bwd_partial_rows(int64_t rows, int n, bool vec, int e) {
   if (vec) {
-    const int64_t rpb = kWavesPerBlock / pick_wpr_bwd(n);
+    const int64_t rpb = kWavesPerBlock / pick_wpr_bwd(n / e);
     const int64_t b = ceil_div(rows, rpb);
     return b < kBwdMaxBlocks ? b : kBwdMaxBlocks;
   }
   return ceil_div(rows, scalar_chunk(rows));
 }
 
+// The most any dtype and path needs, so the workspace size depends on neither.
 int64_t bwd_partial_rows_max(int64_t rows, int n) {
-  const int64_t a = bwd_partial_rows(rows, n, true), b = bwd_partial_rows(rows, n, false);
-  return a > b ? a : b;
+  int64_t m = bwd_partial_rows(rows, n, false, 8);
+  for (int e : {8, 4}) {
+    const int64_t a = bwd_partial_rows(rows, n, true, e);
+    if (a > m) m = a;
+  }
+  return m;
 }
+
+template <int DT>
+int rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows, int n, float eps,
+                hipStream_t st) {
+  using T = typename Elem<DT>::T;
+  constexpr int E = Elem<DT>::E;
+  if (vec_ok(n, E, {x, w, y})) {
+    const int nch = n / E;
+    const int wpr = pick_wpr(nch);
+    const int vpt = pick_vpt(nch, wpr);
+#define KRSI_FWD_CASE(W, V)                                  \
+  if (wpr == W && vpt == V) {                                \
+    launch_fwd<DT, W, V>(x, w, y, rstd, rows, n, eps, st);   \
+    return launch_status();                                  \
+  }
+    KRSI_FWD_CASE(1, 1) KRSI_FWD_CASE(1, 2) KRSI_FWD_CASE(1, 4)
+    KRSI_FWD_CASE(4, 2) KRSI_FWD_CASE(4, 4) KRSI_FWD_CASE(4, 8)
+#undef KRSI_FWD_CASE
+    // Wider than 8 chunks per lane (fp32 rows above 8192): the scalar path.
+  }
+  hipLaunchKernelGGL((rms_fwd_scalar<DT>), dim3((unsigned)ceil_div(rows, kWavesPerBlock)),
+                     dim3(kThreads), 0, st, (const T*)x, (const T*)w, (T*)y, rstd, rows, n, eps);
+  return launch_status();
+}
+
+template <int DT>
+int rmsnorm_bwd(const void* g, const void* x, const void* w, const float* rstd, void* dx, void* dw,
+                void* workspace, int64_t rows, int n, hipStream_t st) {
+  using T = typename Elem<DT>::T;
+  constexpr int E = Elem<DT>::E;
+  float* part = static_cast<float*>(workspace);
+  int64_t p1 = 0;
+  bool done = false;
+  if (vec_ok(n, E, {g, x, w, dx})) {
+    const int nch = n / E;
+    const int wpr = pick_wpr_bwd(nch);
+    const int vpt = pick_vpt(nch, wpr);
+#define KRSI_BWD_CASE(W, V)                                                \
+  if (!done && wpr == W && vpt == V) {                                     \
+    p1 = launch_bwd<DT, W, V>(g, x, w, rstd, dx, part, rows, n, st);       \
+    done = true;                                                           \
+  }
+    KRSI_BWD_CASE(1, 1) KRSI_BWD_CASE(1, 2) KRSI_BWD_CASE(2, 1) KRSI_BWD_CASE(2, 2)
+    KRSI_BWD_CASE(4, 1) KRSI_BWD_CASE(4, 2) KRSI_BWD_CASE(4, 4) KRSI_BWD_CASE(4, 8)
+#undef KRSI_BWD_CASE
+  }
+  if (!done) {
+    hipLaunchKernelGGL((rms_bwd_dx_scalar<DT>), dim3((unsigned)ceil_div(rows, kWavesPerBlock)),
+                       dim3(kThreads), 0, st, (const T*)g, (const T*)x, (const T*)w, rstd, (T*)dx,
+                       rows, n);
+    const int64_t chunk = scalar_chunk(rows);
+    p1 = ceil_div(rows, chunk);
+    hipLaunchKernelGGL((rms_bwd_dw_scalar<DT>), dim3((unsigned)ceil_div(n, kThreads), (unsigned)p1),
+                       dim3(kThreads), 0, st, (const T*)g, (const T*)x, rstd, part, rows, n, chunk);
+  }
+  int rc = launch_status();
+  if (rc != KRSI_OK) return rc;
+  float* part2 = reinterpret_cast<float*>(
+      static_cast<char*>(workspace) +
+      align256((size_t)bwd_partial_rows_max(rows, n) * n * sizeof(float)));
+  const int64_t p2 = ceil_div(p1, kColsumRows);
+  const unsigned ctiles = (unsigned)ceil_div(n, kWave);
+  hipLaunchKernelGGL((colsum<false, DT>), dim3(ctiles, (unsigned)p2), dim3(kThreads), 0, st,
+                     (const float*)part, p1, (int)n, (int64_t)kColsumRows, part2, (T*)nullptr);
+  hipLaunchKernelGGL((colsum<true, DT>), dim3(ctiles, 1), dim3(kThreads), 0, st, (const float*)part2,
+                     p2, (int)n, p2, (float*)nullptr, (T*)dw);
+  return launch_status();
+}
+
+// dw of an empty batch is zero; one column-sum launch over zero rows writes it.
+template <int DT>
+int rmsnorm_bwd_empty(void* dw, int n, hipStream_t st) {
+  using T = typename Elem<DT>::T;
+  hipLaunchKernelGGL((colsum<true, DT>), dim3((unsigned)ceil_div(n, kWave), 1), dim3(kThreads), 0,
+                     st, (const float*)nullptr, (int64_t)0, (int)n, (int64_t)1, (float*)nullptr,
+                     (T*)dw);
+  return launch_status();
+}
+
+bool known_dtype(int32_t dt) { return dt == kBf16 || dt == kF16 || dt == kF32; }
 
 }  // namespace
 
@@ -409,95 +504,72 @@ extern "C" {
 size_t krsi_rmsnorm_bwd_workspace_bytes(int64_t rows, int32_t n) {
   using namespace krsi;
   if (rows <= 0 || n <= 0) return 0;
-  // The larger of the two paths' needs, so the size does not depend on the
-  // pointers' alignment.
   const int64_t p1 = bwd_partial_rows_max(rows, n);
   const int64_t p2 = ceil_div(p1, kColsumRows);
   return align256((size_t)p1 * n * sizeof(float)) + align256((size_t)p2 * n * sizeof(float));
 }
 
-int krsi_rmsnorm_fwd_bf16(const void* x, const void* w, void* y, float* rstd, int64_t rows,
-                          int32_t n, float eps, void* stream) {
+int krsi_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows, int32_t n,
+                     float eps, int32_t dtype, void* stream) {
   using namespace krsi;
+  if (!known_dtype(dtype)) return KRSI_ERR_UNSUPPORTED;
   if (rows < 0 || n <= 0 || n > 16384) return KRSI_ERR_BAD_SHAPE;
   if (!(eps == eps) || eps > 3.0e38f || eps < -3.0e38f) return KRSI_ERR_BAD_SCALE;
   if (rows == 0) return KRSI_OK;
   if (!x || !w || !y || !rstd) return KRSI_ERR_NULL_POINTER;
   hipStream_t st = as_stream(stream);
-  if (vec_ok(n, {x, w, y})) {
-    const int wpr = pick_wpr(n);
-    const int vpt = pick_vpt(n, wpr);
-#define KRSI_FWD_CASE(W, V)                              \
-  if (wpr == W && vpt == V) {                            \
-    launch_fwd<W, V>(x, w, y, rstd, rows, n, eps, st);   \
-    return launch_status();                              \
+  switch (dtype) {
+    case kF16:
+      return rmsnorm_fwd<kF16>(x, w, y, rstd, rows, n, eps, st);
+    case kF32:
+      return rmsnorm_fwd<kF32>(x, w, y, rstd, rows, n, eps, st);
+    default:
+      return rmsnorm_fwd<kBf16>(x, w, y, rstd, rows, n, eps, st);
   }
-    KRSI_FWD_CASE(1, 1) KRSI_FWD_CASE(1, 2) KRSI_FWD_CASE(1, 4)
-    KRSI_FWD_CASE(4, 2) KRSI_FWD_CASE(4, 4) KRSI_FWD_CASE(4, 8)
-#undef KRSI_FWD_CASE
-    return KRSI_ERR_UNSUPPORTED;
-  }
-  hipLaunchKernelGGL(rms_fwd_scalar, dim3((unsigned)ceil_div(rows, kWavesPerBlock)), dim3(kThreads),
-                     0, st, (const uint16_t*)x, (const uint16_t*)w, (uint16_t*)y, rstd, rows, n,
-                     eps);
-  return launch_status();
 }
 
-int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const float* rstd, void* dx,
-                          void* dw, void* workspace, size_t workspace_bytes, int64_t rows,
-                          int32_t n, void* stream) {
+int krsi_rmsnorm_bwd(const void* g, const void* x, const void* w, const float* rstd, void* dx,
+                     void* dw, void* workspace, size_t workspace_bytes, int64_t rows, int32_t n,
+                     int32_t dtype, void* stream) {
   using namespace krsi;
+  if (!known_dtype(dtype)) return KRSI_ERR_UNSUPPORTED;
   if (rows < 0 || n <= 0 || n > 16384) return KRSI_ERR_BAD_SHAPE;
   if (!dw) return KRSI_ERR_NULL_POINTER;
   hipStream_t st = as_stream(stream);
   if (rows == 0) {
-    // dw of an empty batch is zero; one column-sum launch over zero rows writes it.
-    hipLaunchKernelGGL((colsum<true>), dim3((unsigned)ceil_div(n, kWave), 1), dim3(kThreads), 0,
-                       st, (const float*)nullptr, (int64_t)0, (int)n, (int64_t)1, (float*)nullptr,
-                       (uint16_t*)dw);
-    return launch_status();
+    switch (dtype) {
+      case kF16:
+        return rmsnorm_bwd_empty<kF16>(dw, n, st);
+      case kF32:
+        return rmsnorm_bwd_empty<kF32>(dw, n, st);
+      default:
+        return rmsnorm_bwd_empty<kBf16>(dw, n, st);
+    }
   }
   if (!g || !x || !w || !rstd || !dx) return KRSI_ERR_NULL_POINTER;
   const size_t need = krsi_rmsnorm_bwd_workspace_bytes(rows, n);
   if (!workspace || workspace_bytes < need) return KRSI_ERR_WORKSPACE;
   if (!aligned16(workspace)) return KRSI_ERR_MISALIGNED;
-  float* part = static_cast<float*>(workspace);
-  int64_t p1 = 0;
-  if (vec_ok(n, {g, x, w, dx})) {
-    const int wpr = pick_wpr_bwd(n);
-    const int vpt = pick_vpt(n, wpr);
-    bool done = false;
-#define KRSI_BWD_CASE(W, V)                                            \
-  if (!done && wpr == W && vpt == V) {                                 \
-    p1 = launch_bwd<W, V>(g, x, w, rstd, dx, part, rows, n, st);       \
-    done = true;                                                       \
+  switch (dtype) {
+    case kF16:
+      return rmsnorm_bwd<kF16>(g, x, w, rstd, dx, dw, workspace, rows, n, st);
+    case kF32:
+      return rmsnorm_bwd<kF32>(g, x, w, rstd, dx, dw, workspace, rows, n, st);
+    default:
+      return rmsnorm_bwd<kBf16>(g, x, w, rstd, dx, dw, workspace, rows, n, st);
   }
-    KRSI_BWD_CASE(1, 1) KRSI_BWD_CASE(1, 2) KRSI_BWD_CASE(2, 1) KRSI_BWD_CASE(2, 2)
-    KRSI_BWD_CASE(4, 1) KRSI_BWD_CASE(4, 2) KRSI_BWD_CASE(4, 4) KRSI_BWD_CASE(4, 8)
-#undef KRSI_BWD_CASE
-    if (!done) return KRSI_ERR_UNSUPPORTED;
-  } else {
-    hipLaunchKernelGGL(rms_bwd_dx_scalar, dim3((unsigned)ceil_div(rows, kWavesPerBlock)),
-                       dim3(kThreads), 0, st, (const uint16_t*)g, (const uint16_t*)x,
-                       (const uint16_t*)w, rstd, (uint16_t*)dx, rows, n);
-    const int64_t chunk = scalar_chunk(rows);
-    p1 = ceil_div(rows, chunk);
-    hipLaunchKernelGGL(rms_bwd_dw_scalar, dim3((unsigned)ceil_div(n, kThreads), (unsigned)p1),
-                       dim3(kThreads), 0, st, (const uint16_t*)g, (const uint16_t*)x, rstd, part,
-                       rows, n, chunk);
-  }
-  int rc = launch_status();
-  if (rc != KRSI_OK) return rc;
-  float* part2 = reinterpret_cast<float*>(
-      static_cast<char*>(workspace) +
-      align256((size_t)bwd_partial_rows_max(rows, n) * n * sizeof(float)));
-  const int64_t p2 = ceil_div(p1, kColsumRows);
-  const unsigned ctiles = (unsigned)ceil_div(n, kWave);
-  hipLaunchKernelGGL((colsum<false>), dim3(ctiles, (unsigned)p2), dim3(kThreads), 0, st,
-                     (const float*)part, p1, (int)n, (int64_t)kColsumRows, part2, (uint16_t*)nullptr);
-  hipLaunchKernelGGL((colsum<true>), dim3(ctiles, 1), dim3(kThreads), 0, st, (const float*)part2,
-                     p2, (int)n, p2, (float*)nullptr, (uint16_t*)dw);
-  return launch_status();
+}
+
+int krsi_rmsnorm_fwd_bf16(const void* x, const void* w, void* y, float* rstd, int64_t rows,
+                          int32_t n, float eps, void* stream) {
+  return krsi_rmsnorm_fwd(x, w, y, rstd, rows, n, eps, KRSI_DTYPE_BF16, stream);
+}
+
+int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const float* rstd, void* dx,
+                          void* dw, void* workspace, size_t workspace_bytes, int64_t rows,
+                          int32_t n, void* stream) {
+  return krsi_rmsnorm_bwd(g, x, w, rstd, dx, dw, workspace, workspace_bytes, rows, n,
+                          KRSI_DTYPE_BF16, stream);
 }
 
 }  // extern "C"

@@ -14,7 +14,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LIB_PATH = Path(__file__).resolve().parent.parent / "libkrsi_hip.so"
 
 # Names and signatures of every entry point of include/krsi.h.
@@ -22,16 +22,27 @@ _P, _I32, _I64, _F32, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, cty
 SIGNATURES = {
     "krsi_abi_version": (ctypes.c_int, []),
     "krsi_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "krsi_rmsnorm_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _F32, _I32, _P]),
     "krsi_rmsnorm_fwd_bf16": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I32, _F32, _P]),
     "krsi_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I32]),
+    "krsi_rmsnorm_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I32, _I32, _P]),
     "krsi_rmsnorm_bwd_bf16": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I32, _P]),
+    "krsi_geglu_fwd": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P]),
     "krsi_geglu_fwd_bf16": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P]),
+    "krsi_geglu_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _I32, _P]),
     "krsi_geglu_bwd_bf16": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P]),
+    "krsi_relpos_fwd": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _I32, _P]),
     "krsi_relpos_fwd_bf16": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _P]),
     "krsi_relpos_bwd_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "krsi_relpos_bwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _SZ,
+                                       _I32, _I32, _I32, _I32, _F32, _I32, _P]),
     "krsi_relpos_bwd_bf16": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _SZ,
                                             _I32, _I32, _I32, _I32, _F32, _P]),
 }
+
+# KRSI_DTYPE_* codes of the activation dtypes.
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+_ATTN_DTYPES = (torch.bfloat16, torch.float16)
 
 _lib = None
 _lock = threading.Lock()
@@ -80,9 +91,15 @@ def _on_gpu(*ts: torch.Tensor) -> None:
             raise ValueError(f"tensors on different devices: {dev} and {t.device}")
 
 
-def _bf16(name: str, t: torch.Tensor) -> None:
-    if t.dtype != torch.bfloat16:
-        raise TypeError(f"{name} must be torch.bfloat16, got {t.dtype}")
+def _dtype(name: str, t: torch.Tensor, like: torch.Tensor | None = None,
+           allowed: tuple = tuple(DTYPE_CODES)) -> int:
+    """KRSI_DTYPE_* code of t, which must be one of `allowed` and, if given, of like's dtype."""
+    if t.dtype not in allowed:
+        names = ", ".join(str(d) for d in allowed)
+        raise TypeError(f"{name} must be one of {names}, got {t.dtype}")
+    if like is not None and t.dtype != like.dtype:
+        raise TypeError(f"{name} must have the dtype of the activations ({like.dtype}), got {t.dtype}")
+    return DTYPE_CODES[t.dtype]
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -91,10 +108,10 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 # ------------------------------------------------------------------- RMSNorm
 def rmsnorm_fwd(x2d: torch.Tensor, w: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """y, rstd for a contiguous [rows, N] bf16 x2d and [N] bf16 weight."""
+    """y, rstd for a contiguous [rows, N] x2d and [N] weight of one dtype (bf16, fp16 or fp32)."""
     _on_gpu(x2d, w)
-    _bf16("x2d", x2d)
-    _bf16("weight", w)
+    dt = _dtype("x2d", x2d)
+    _dtype("weight", w, like=x2d)
     if x2d.dim() != 2 or not x2d.is_contiguous():
         raise ValueError("x2d must be a contiguous 2D tensor [rows, N]")
     rows, n = x2d.shape
@@ -104,27 +121,29 @@ def rmsnorm_fwd(x2d: torch.Tensor, w: torch.Tensor, eps: float) -> tuple[torch.T
     y = torch.empty_like(x2d)
     rstd = torch.empty(rows, device=x2d.device, dtype=torch.float32)
     if rows:
-        _check(lib().krsi_rmsnorm_fwd_bf16(_ptr(x2d), _ptr(w), _ptr(y), _ptr(rstd), rows, n,
-                                           float(eps), _stream(x2d)))
+        _check(lib().krsi_rmsnorm_fwd(_ptr(x2d), _ptr(w), _ptr(y), _ptr(rstd), rows, n,
+                                      float(eps), dt, _stream(x2d)))
     return y, rstd
 
 
 def rmsnorm_bwd(g: torch.Tensor, x2d: torch.Tensor, w: torch.Tensor,
                 rstd: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """dx (bf16) and dw (bf16, fp32-accumulated) of rmsnorm."""
+    """dx and dw (fp32-accumulated) of rmsnorm, in the dtype of x2d."""
     _on_gpu(g, x2d, w, rstd)
     g = g.contiguous()
     w = w.contiguous()
     rows, n = x2d.shape
     if g.shape != x2d.shape:
         raise ValueError(f"grad shape {tuple(g.shape)} != {tuple(x2d.shape)}")
-    _bf16("grad", g)
+    dt = _dtype("x2d", x2d)
+    _dtype("weight", w, like=x2d)
+    _dtype("grad", g, like=x2d)
     dx = torch.empty_like(x2d)
     dw = torch.empty(n, device=x2d.device, dtype=w.dtype)
     nbytes = lib().krsi_rmsnorm_bwd_workspace_bytes(rows, n)
     ws = torch.empty(max(nbytes, 1), device=x2d.device, dtype=torch.uint8)
-    _check(lib().krsi_rmsnorm_bwd_bf16(_ptr(g), _ptr(x2d), _ptr(w), _ptr(rstd), _ptr(dx), _ptr(dw),
-                                       _ptr(ws), nbytes, rows, n, _stream(x2d)))
+    _check(lib().krsi_rmsnorm_bwd(_ptr(g), _ptr(x2d), _ptr(w), _ptr(rstd), _ptr(dx), _ptr(dw),
+                                  _ptr(ws), nbytes, rows, n, dt, _stream(x2d)))
     return dx, dw
 
 
@@ -140,35 +159,36 @@ def _approx(approximate: str) -> int:
 
 def geglu_fwd(u: torch.Tensor, approximate: str = "tanh") -> torch.Tensor:
     _on_gpu(u)
-    _bf16("u", u)
+    dt = _dtype("u", u)
     if u.dim() != 2 or not u.is_contiguous() or u.shape[1] % 2:
         raise ValueError("u must be a contiguous [rows, 2F] tensor")
     rows, f2 = u.shape
     out = torch.empty(rows, f2 // 2, device=u.device, dtype=u.dtype)
     if rows and f2:
-        _check(lib().krsi_geglu_fwd_bf16(_ptr(u), _ptr(out), rows, f2 // 2, _approx(approximate),
-                                         _stream(u)))
+        _check(lib().krsi_geglu_fwd(_ptr(u), _ptr(out), rows, f2 // 2, _approx(approximate), dt,
+                                    _stream(u)))
     return out
 
 
 def geglu_bwd(g: torch.Tensor, u: torch.Tensor, approximate: str = "tanh") -> torch.Tensor:
     _on_gpu(g, u)
     g = g.contiguous()
-    _bf16("grad", g)
+    dt = _dtype("u", u)
+    _dtype("grad", g, like=u)
     rows, f2 = u.shape
     if g.shape != (rows, f2 // 2):
         raise ValueError(f"grad shape {tuple(g.shape)} != {(rows, f2 // 2)}")
     du = torch.empty_like(u)
     if rows and f2:
-        _check(lib().krsi_geglu_bwd_bf16(_ptr(g), _ptr(u), _ptr(du), rows, f2 // 2,
-                                         _approx(approximate), _stream(u)))
+        _check(lib().krsi_geglu_bwd(_ptr(g), _ptr(u), _ptr(du), rows, f2 // 2,
+                                    _approx(approximate), dt, _stream(u)))
     return du
 
 
 # ------------------------------------------------ relative-position attention
-def _check_relpos(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: int) -> None:
+def _check_relpos(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: int) -> int:
     _on_gpu(qkv, pd)
-    _bf16("qkv", qkv)
+    dt = _dtype("qkv", qkv, allowed=_ATTN_DTYPES)
     if pd.dtype != torch.float32:
         raise TypeError(f"pd must be torch.float32, got {pd.dtype}")
     if qkv.dim() != 2 or qkv.stride(1) != 1:
@@ -179,18 +199,19 @@ def _check_relpos(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D
         raise ValueError(f"pd shape {tuple(pd.shape)} != {(H, 2 * S - 1)}")
     if D % 8 or not 8 <= D <= 128:
         raise ValueError(f"head dim D={D} unsupported: needs D % 8 == 0 and 8 <= D <= 128")
+    return dt
 
 
 def relpos_fwd(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: int,
                scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """out (bf16), out32 (fp32) [B*S, H*D] and lse [B*H, S] (log2 domain)."""
-    _check_relpos(qkv, pd, B, S, H, D)
+    """out (qkv's dtype), out32 (fp32) [B*S, H*D] and lse [B*H, S] (log2 domain)."""
+    dt = _check_relpos(qkv, pd, B, S, H, D)
     pd = pd.contiguous()
     out = torch.empty(B * S, H * D, device=qkv.device, dtype=qkv.dtype)
     out32 = torch.empty(B * S, H * D, device=qkv.device, dtype=torch.float32)
     lse = torch.empty(B * H, S, device=qkv.device, dtype=torch.float32)
-    _check(lib().krsi_relpos_fwd_bf16(_ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out), _ptr(out32),
-                                      _ptr(lse), B, S, H, D, float(scale), _stream(qkv)))
+    _check(lib().krsi_relpos_fwd(_ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out), _ptr(out32),
+                                 _ptr(lse), B, S, H, D, float(scale), dt, _stream(qkv)))
     return out, out32, lse
 
 
@@ -198,10 +219,10 @@ def relpos_bwd(dout: torch.Tensor, qkv: torch.Tensor, pd: torch.Tensor, out32: t
                lse: torch.Tensor, B: int, S: int, H: int, D: int,
                scale: float) -> tuple[torch.Tensor, torch.Tensor]:
     """dqkv (same shape and strides as a contiguous qkv) and dpd [H, 2S-1] fp32."""
-    _check_relpos(qkv, pd, B, S, H, D)
+    dt = _check_relpos(qkv, pd, B, S, H, D)
     _on_gpu(dout, out32, lse)
     dout = dout.contiguous()
-    _bf16("grad", dout)
+    _dtype("grad", dout, like=qkv)
     pd = pd.contiguous()
     # Every column of dqkv is written (q, k and v slots of each head); columns
     # past 3*H*D of a wider qkv are zero, as the gradient of a slice.
@@ -211,7 +232,7 @@ def relpos_bwd(dout: torch.Tensor, qkv: torch.Tensor, pd: torch.Tensor, out32: t
     dpd = torch.empty(H, 2 * S - 1, device=qkv.device, dtype=torch.float32)
     nbytes = lib().krsi_relpos_bwd_workspace_bytes(B, S, H, D)
     ws = torch.empty(nbytes, device=qkv.device, dtype=torch.uint8)
-    _check(lib().krsi_relpos_bwd_bf16(_ptr(dout), _ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out32),
-                                      _ptr(lse), _ptr(dqkv), dqkv.stride(0), _ptr(dpd), _ptr(ws), nbytes,
-                                      B, S, H, D, float(scale), _stream(qkv)))
+    _check(lib().krsi_relpos_bwd(_ptr(dout), _ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out32),
+                                 _ptr(lse), _ptr(dqkv), dqkv.stride(0), _ptr(dpd), _ptr(ws), nbytes,
+                                 B, S, H, D, float(scale), dt, _stream(qkv)))
     return dqkv, dpd

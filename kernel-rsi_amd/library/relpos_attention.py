@@ -1,5 +1,5 @@
 """Flash attention forward + backward with an additive bias that depends only on (j - i), on
-hand-written gfx950 (MI355X) HIP kernels (bf16 MFMA, fp32 softmax).
+hand-written gfx950 (MI355X) HIP kernels (bf16 or fp16 MFMA, fp32 softmax).
 
 relpos_attention(qkv, pd, B, S, H, D, scale) -> [B*S, H*D]   (differentiable, torch.compile-friendly)
   qkv: [B*S, 3*H*D] (the fused q|k|v GEMM output, read in place: no permute copies; any row stride)

@@ -13,7 +13,8 @@ Three layers, each pinning the next:
      by). relpos uses explicit matmul + softmax in fp32 and the reference's SDPA-MATH
      formulation (`relpos_sdpa`) is kept to cross-check it.
   3. `bf16_round` - round-to-nearest-even to bfloat16 emulated with integer arithmetic in
-     numpy, used to pin the rounding points of layer 2's bf16 runs.
+     numpy, used to pin the rounding points of layer 2's bf16 runs; fp16 runs are pinned
+     against numpy's own IEEE binary16 conversion (`f16_round`), fp32 runs need none.
 
 Reference files followed (kernel-rsi, read, not run):
   rmsnorm          library/rmsnorm.py:113-115 (reference), :22-51 (kernel math)
@@ -44,6 +45,13 @@ def bf16_round(a: np.ndarray) -> np.ndarray:
     nan = np.isnan(a)
     out[nan] = a[nan]
     return out
+
+
+def f16_round(a: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest IEEE binary16 (ties to even, subnormals kept,
+    overflow to inf) with numpy's conversion, independent of torch; returned as float32."""
+    with np.errstate(over="ignore"):
+        return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
 def to_bf16_exact(t: torch.Tensor) -> torch.Tensor:
@@ -79,6 +87,13 @@ def rmsnorm_np64(x: np.ndarray, w: np.ndarray, eps: float, g: np.ndarray):
     dx = r * gw - x * r ** 3 * (gw * x).sum(-1, keepdims=True) / n
     dw = (g * x * r).sum(0)
     return y, r[:, 0], dx, dw
+
+
+def rmsnorm_eager_np(x: np.ndarray, w: np.ndarray, eps: float, rnd) -> np.ndarray:
+    """rmsnorm_eager_bf16_np with the rounding function `rnd` of the activation dtype."""
+    x = np.asarray(x, np.float32)
+    r = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True, dtype=np.float32) + np.float32(eps))
+    return rnd(np.asarray(w, np.float32) * rnd(x * r))
 
 
 def rmsnorm_eager_bf16_np(x_bf: np.ndarray, w_bf: np.ndarray, eps: float) -> np.ndarray:
@@ -183,19 +198,22 @@ def diag_sum(ds: torch.Tensor, S: int) -> torch.Tensor:
     return out.index_add_(1, idx, ds.reshape(H, S * S))
 
 
-def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False):
+def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False, eager_dtype=None):
     """Forward and backward of the reference in explicit fp32 math with contiguous matmul
-    operands (device-agnostic; no bf16 batched product is ever formed).
-      eager_bf16=False: the fp32 reference (ref32) of bf16 inputs.
-      eager_bf16=True : the eager bf16 original as torch runs it - SDPA-MATH upcasts bf16 to
-                        fp32 internally, so it is this fp32 math with the bias rounded to bf16
-                        (relpos_attention.py:207), out and dqkv rounded to bf16, and dpd the
-                        fp32 diagonal sum of bf16-rounded dS (the gather's backward).
+    operands (device-agnostic; no 16-bit batched product is ever formed).
+      no eager dtype : the fp32 reference (ref32) of the (16-bit) inputs.
+      eager_dtype=T  : the eager original in dtype T (bf16 or fp16) as torch runs it -
+                       SDPA-MATH upcasts 16-bit inputs to fp32 internally, so it is this fp32
+                       math with the bias rounded to T (relpos_attention.py:207), out and dqkv
+                       rounded to T, and dpd the fp32 diagonal sum of T-rounded dS (the
+                       gather's backward). eager_bf16=True is eager_dtype=torch.bfloat16.
     Returns (out [B*S, H*D], lse [B*H, S] log2 domain, dqkv [B*S, 3*H*D], dpd [H, 2S-1])."""
+    if eager_bf16:
+        eager_dtype = torch.bfloat16
     q, k, v = (t.float().contiguous() for t in split_qkv(qkv, B, S, H, D))
     bias = bias_matrix(pd.float(), S)[None]
-    if eager_bf16:
-        bias = bias.to(torch.bfloat16).float()
+    if eager_dtype is not None:
+        bias = bias.to(eager_dtype).float()
     s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale + bias
     lse = torch.logsumexp(s, dim=-1)
     p = torch.exp(s - lse[..., None])
@@ -210,28 +228,29 @@ def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False):
     del p
     dq = torch.matmul(ds, k) * scale
     dk = torch.matmul(ds.transpose(-2, -1).contiguous(), q) * scale
-    if eager_bf16:
-        ds = ds.to(torch.bfloat16).float()
+    if eager_dtype is not None:
+        ds = ds.to(eager_dtype).float()
     dpd = diag_sum(ds, S)
     del ds
     out = o.permute(0, 2, 1, 3).reshape(B * S, H * D)
     dqkv = torch.stack([dq, dk, dv], dim=2).permute(0, 3, 2, 1, 4).reshape(B * S, 3 * H * D)
-    if eager_bf16:
-        out, dqkv = out.to(torch.bfloat16), dqkv.to(torch.bfloat16)
+    if eager_dtype is not None:
+        out, dqkv = out.to(eager_dtype), dqkv.to(eager_dtype)
     return out, (lse * LOG2E).reshape(B * H, S), dqkv, dpd
 
 
-def relpos_kernel_emulated(qkv, pd, B, S, H, D, scale, dout):
+def relpos_kernel_emulated(qkv, pd, B, S, H, D, scale, dout, dtype=torch.bfloat16):
     """The reference Triton kernels' rounding points, in fp32 math with contiguous operands
-    (the yardstick "the reference kernel's own error"):
-      forward  acc = bf16(p_u) v with p_u = exp(s - rowmax), l = sum p_u (fp32), o = acc / l,
-               stored as out32 (fp32) and out (bf16)                 (relpos_attention.py:49-58)
-      backward p = exp(s - lse) fp32, dv = bf16(p)^T dO (:88), dp = dO v^T (:89),
+    (the yardstick "the reference kernel's own error"), for activations of `dtype` (T, the
+    dtype of q, k and v: bf16 or fp16):
+      forward  acc = T(p_u) v with p_u = exp(s - rowmax), l = sum p_u (fp32), o = acc / l,
+               stored as out32 (fp32) and out (T)                    (relpos_attention.py:49-58)
+      backward p = exp(s - lse) fp32, dv = T(p)^T dO (:88), dp = dO v^T (:89),
                delta = sum dO * out32 (:144), ds = p (dp - delta) (:90),
-               dk = scale bf16(ds)^T q (:92-93), dq = scale bf16(ds) k (:125-126),
-               dpd = diagonal sums of fp32 ds (:91, :154-156); dqkv rounded to bf16.
-    Returns (out bf16, dqkv bf16, dpd fp32)."""
-    bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+               dk = scale T(ds)^T q (:92-93), dq = scale T(ds) k (:125-126),
+               dpd = diagonal sums of fp32 ds (:91, :154-156); dqkv rounded to T.
+    Returns (out T, dqkv T, dpd fp32)."""
+    bf = lambda t: t.to(dtype).float()  # noqa: E731
     q, k, v = (t.float().contiguous() for t in split_qkv(qkv, B, S, H, D))
     s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale + bias_matrix(pd.float(), S)[None]
     m = s.amax(-1, keepdim=True)
@@ -253,9 +272,9 @@ def relpos_kernel_emulated(qkv, pd, B, S, H, D, scale, dout):
     dk = torch.matmul(dsb.transpose(-2, -1).contiguous(), q) * scale
     del dsb
     dpd = diag_sum(ds, S)
-    out = o32.permute(0, 2, 1, 3).reshape(B * S, H * D).to(torch.bfloat16)
+    out = o32.permute(0, 2, 1, 3).reshape(B * S, H * D).to(dtype)
     dqkv = torch.stack([dq, dk, dv], dim=2).permute(0, 3, 2, 1, 4).reshape(B * S, 3 * H * D)
-    return out, dqkv.to(torch.bfloat16), dpd
+    return out, dqkv.to(dtype), dpd
 
 
 def relpos_np64(qkv: np.ndarray, pd: np.ndarray, B, S, H, D, scale, dout: np.ndarray):

@@ -98,6 +98,31 @@ def test_validation_before_launch():
                                     2, 16, 2, 64, 0.125, NULL) == E["SHAPE"]
 
 
+def test_dtype_argument_validated_before_launch():
+    """The generic entry points take KRSI_DTYPE_* (0 bf16, 1 fp16, 2 fp32); an unknown code,
+    or fp32 for attention, is UNSUPPORTED before anything is launched (FAKE pointers)."""
+    lib = _hip.lib()
+    UNSUP, NULLP = 5, 1
+    for dt in (-1, 3, 99):
+        assert lib.krsi_rmsnorm_fwd(FAKE, FAKE, FAKE, FAKE, 4, 64, 1e-6, dt, NULL) == UNSUP
+        assert lib.krsi_rmsnorm_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, 4, 64, dt, NULL) == UNSUP
+        assert lib.krsi_geglu_fwd(FAKE, FAKE, 4, 8, 1, dt, NULL) == UNSUP
+        assert lib.krsi_geglu_bwd(FAKE, FAKE, FAKE, 4, 8, 1, dt, NULL) == UNSUP
+    for dt in (2, 3):
+        assert lib.krsi_relpos_fwd(FAKE, 384, FAKE, FAKE, FAKE, FAKE, 2, 16, 2, 64, 0.125, dt, NULL) == UNSUP
+        assert lib.krsi_relpos_bwd(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 384, FAKE, FAKE, 1 << 30,
+                                   2, 16, 2, 64, 0.125, dt, NULL) == UNSUP
+    # Known dtypes reach the usual checks (here: a NULL pointer), still before any launch.
+    for dt in (0, 1, 2):
+        assert lib.krsi_rmsnorm_fwd(NULL, FAKE, FAKE, FAKE, 4, 64, 1e-6, dt, NULL) == NULLP
+        assert lib.krsi_geglu_fwd(NULL, FAKE, 4, 8, 1, dt, NULL) == NULLP
+    for dt in (0, 1):
+        assert lib.krsi_relpos_fwd(FAKE, 384, NULL, FAKE, FAKE, FAKE, 2, 16, 2, 64, 0.125, dt, NULL) == NULLP
+    # The workspace size does not depend on the dtype: one size serves all three.
+    assert lib.krsi_rmsnorm_bwd_workspace_bytes(1000, 16384) >= 512 * 16384 * 4
+    assert _hip.DTYPE_CODES == {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
 def test_python_layer_has_no_cpu_path():
     import geglu
     import relpos_attention

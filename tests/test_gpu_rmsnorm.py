@@ -97,5 +97,6 @@ def test_rmsnorm_backward_deterministic():
 def test_rmsnorm_rejects_cpu_and_wrong_dtype():
     with pytest.raises(ValueError):
         R.rmsnorm(torch.randn(4, 8, dtype=torch.bfloat16), torch.ones(8, dtype=torch.bfloat16), EPS)
-    with pytest.raises(TypeError):
-        R.rmsnorm(torch.randn(4, 8, device="cuda"), torch.ones(8, device="cuda"), EPS)
+    with pytest.raises(TypeError):  # float64 is not an activation dtype of the kernels
+        R.rmsnorm(torch.randn(4, 8, device="cuda", dtype=torch.float64),
+                  torch.ones(8, device="cuda", dtype=torch.float64), EPS)

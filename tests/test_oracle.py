@@ -230,3 +230,58 @@ def test_geglu_erf_approximation_bound():
     ref = np.array([math.erf(float(v)) for v in x])
     assert np.abs(y.astype(np.float64) - ref).max() < 6e-7
     assert y[0] == -1.0 and y[-1] == 1.0 and y[len(x) // 2] == 0.0
+
+
+# ---------------------------------------------------------- fp16 rounding points
+def test_f16_round_matches_torch_including_ties_and_subnormals():
+    """The oracle's fp16 runs round with torch's .to(float16); numpy's binary16 conversion
+    (an independent implementation) agrees on normals, exact ties, subnormals and overflow."""
+    gen = torch.Generator().manual_seed(14)
+    a = (torch.randn(100000, generator=gen) * 300).numpy()
+    base = np.float32([1.0, 1.5, -3.0, 0.3, 2.0 ** -20])       # 2^-20 is subnormal in fp16
+    ulp = np.float32([2.0 ** -10, 2.0 ** -10, 2.0 ** -9, 2.0 ** -12, 2.0 ** -24])
+    ties = base + ulp / 2                                        # exactly half-way
+    a = np.concatenate([a, ties, np.float32([0.0, -0.0, 1e-8, 6e-8, 65504.0, 65519.0, 65520.0, 1e6])])
+    ref = torch.from_numpy(a).to(torch.float16).float().numpy()
+    np.testing.assert_array_equal(O.f16_round(a), ref)
+    assert O.f16_round(np.float32([65520.0]))[0] == np.inf
+
+
+def test_rmsnorm_rounding_points_pinned_fp16():
+    """fp16 run of the oracle: x*r rounded to fp16 before * w, as in the bf16 case."""
+    x = O.randn((256, 1152), 15, dtype=torch.float16)
+    w = O.randn((1152,), 16, std=0.02, mean=1.0, dtype=torch.float16)
+    y = O.rmsnorm(x, w, 1e-6).float().numpy()
+    emu = O.rmsnorm_eager_np(x.float().numpy(), w.float().numpy(), 1e-6, O.f16_round)
+    assert (emu == y).mean() > 0.999
+    xf = x.float().numpy()
+    r = 1.0 / np.sqrt((xf * xf).mean(-1, keepdims=True, dtype=np.float32) + np.float32(1e-6))
+    planted = O.f16_round(w.float().numpy() * (xf * r))
+    assert (planted == y).mean() < 0.95
+
+
+def test_eager_emulation_matches_sdpa_fp16():
+    """oracle.relpos_manual(eager_dtype=fp16) reproduces the eager fp16 run of the reference
+    (SDPA-MATH): out within one fp16 rounding, dqkv up to fp32 summation order."""
+    B, S, H, D = 2, 33, 2, 16
+    qkv = O.randn((B * S, 3 * H * D), 8, std=0.6, dtype=torch.float16)
+    pd = O.randn((H, 2 * S - 1), 9, dtype=torch.float32)
+    dout = O.randn((B * S, H * D), 10, dtype=torch.float16)
+    ob, dqb, dpb = O.relpos_train(qkv, pd, B, S, H, D, 1.0, dout, torch.float16, sdpa=True)
+    e = O.relpos_manual(qkv, pd, B, S, H, D, 1.0, dout, eager_dtype=torch.float16)
+    assert e[0].dtype == torch.float16 and e[2].dtype == torch.float16
+    assert (e[0] == ob).float().mean() > 0.99
+    assert (e[2] == dqb).float().mean() > 0.98
+    assert ((e[3] - dpb).norm() / dpb.norm()) < 1e-2
+
+
+def test_kernel_emulation_fp16_is_close_to_fp32():
+    B, S, H, D = 1, 40, 2, 16
+    qkv = O.randn((B * S, 3 * H * D), 11, dtype=torch.float16)
+    pd = O.randn((H, 2 * S - 1), 12, std=0.3, dtype=torch.float32)
+    dout = O.randn((B * S, H * D), 13, dtype=torch.float16)
+    r = O.relpos_manual(qkv, pd, B, S, H, D, 0.25, dout)
+    k = O.relpos_kernel_emulated(qkv, pd, B, S, H, D, 0.25, dout, dtype=torch.float16)
+    assert k[0].dtype == torch.float16
+    for a, b in ((k[0], r[0]), (k[1], r[2]), (k[2], r[3])):
+        assert ((a.float() - b).norm() / b.norm()) < 5e-3
