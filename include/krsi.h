@@ -139,6 +139,26 @@ int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, cons
                          float* dpd, void* workspace, size_t workspace_bytes, int32_t B,
                          int32_t S, int32_t H, int32_t D, float scale, void* stream);
 
+/* ------------------------------------ bucketed relative-position table (T5)
+ * The steps either side of the attention when pd comes from a bucketed table
+ * (an nn.Embedding [num_buckets, H] indexed by the bucket of j - i, as in T5).
+ * The reference names this step without code (LESSONS.md:35: sum dBias along
+ * the diagonals into [H, 2S-1], then into the buckets, with no scatter); the
+ * attention backward above produces dpd [H, 2S-1], these finish the chain.
+ * bucket: [2S-1] int32 device array, bucket[r] for distance j - i = r - (S-1)
+ * (any map; T5's is built by the Python layer with the T5 formula).
+ *
+ * Gather: pd[h, r] = table[bucket[r] * H + h]; table [num_buckets, H] fp32,
+ * pd [H, 2S-1] fp32. A bucket outside [0, num_buckets) writes NaN.        */
+int krsi_relpos_bucket_gather(const float* table, const int32_t* bucket, float* pd, int32_t S,
+                              int32_t H, int32_t num_buckets, void* stream);
+
+/* Bucket sum (the gather's backward): dtable[b * H + h] = sum of dpd[h, r]
+ * over r with bucket[r] == b, added in a fixed order (bitwise reproducible,
+ * no atomics); every entry of dtable [num_buckets, H] is written.          */
+int krsi_relpos_bucket_sum(const float* dpd, const int32_t* bucket, float* dtable, int32_t S,
+                           int32_t H, int32_t num_buckets, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

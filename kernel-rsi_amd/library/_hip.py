@@ -38,6 +38,8 @@ SIGNATURES = {
                                        _I32, _I32, _I32, _I32, _F32, _I32, _P]),
     "krsi_relpos_bwd_bf16": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _SZ,
                                             _I32, _I32, _I32, _I32, _F32, _P]),
+    "krsi_relpos_bucket_gather": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _P]),
+    "krsi_relpos_bucket_sum": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _P]),
 }
 
 # KRSI_DTYPE_* codes of the activation dtypes.
@@ -236,3 +238,39 @@ def relpos_bwd(dout: torch.Tensor, qkv: torch.Tensor, pd: torch.Tensor, out32: t
                                  _ptr(lse), _ptr(dqkv), dqkv.stride(0), _ptr(dpd), _ptr(ws), nbytes,
                                  B, S, H, D, float(scale), dt, _stream(qkv)))
     return dqkv, dpd
+
+
+# ------------------------------------------ bucketed relative-position table
+def _check_bucket(bucket: torch.Tensor, S: int) -> None:
+    if bucket.dtype != torch.int32 or bucket.dim() != 1 or bucket.numel() != 2 * S - 1:
+        raise ValueError(f"bucket must be a [2S-1] = [{2 * S - 1}] int32 tensor, got "
+                         f"{bucket.dtype} {tuple(bucket.shape)}")
+
+
+def relpos_bucket_gather(table: torch.Tensor, bucket: torch.Tensor, S: int) -> torch.Tensor:
+    """pd [H, 2S-1] fp32 with pd[h, r] = table[bucket[r], h]; table [num_buckets, H] fp32."""
+    _on_gpu(table, bucket)
+    if table.dtype != torch.float32 or table.dim() != 2:
+        raise TypeError(f"table must be a [num_buckets, H] float32 tensor, got {table.dtype} "
+                        f"{tuple(table.shape)}")
+    _check_bucket(bucket, S)
+    table, bucket = table.contiguous(), bucket.contiguous()
+    nb, H = table.shape
+    pd = torch.empty(H, 2 * S - 1, device=table.device, dtype=torch.float32)
+    _check(lib().krsi_relpos_bucket_gather(_ptr(table), _ptr(bucket), _ptr(pd), S, H, nb,
+                                           _stream(table)))
+    return pd
+
+
+def relpos_bucket_sum(dpd: torch.Tensor, bucket: torch.Tensor, S: int, num_buckets: int) -> torch.Tensor:
+    """dtable [num_buckets, H] fp32: the sums of dpd [H, 2S-1] over each bucket's distances."""
+    _on_gpu(dpd, bucket)
+    if dpd.dtype != torch.float32 or dpd.dim() != 2 or dpd.shape[1] != 2 * S - 1:
+        raise ValueError(f"dpd must be an [H, {2 * S - 1}] float32 tensor, got {dpd.dtype} {tuple(dpd.shape)}")
+    _check_bucket(bucket, S)
+    dpd, bucket = dpd.contiguous(), bucket.contiguous()
+    H = dpd.shape[0]
+    dtable = torch.empty(num_buckets, H, device=dpd.device, dtype=torch.float32)
+    _check(lib().krsi_relpos_bucket_sum(_ptr(dpd), _ptr(bucket), _ptr(dtable), S, H, num_buckets,
+                                        _stream(dpd)))
+    return dtable

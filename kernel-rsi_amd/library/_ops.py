@@ -6,7 +6,8 @@ replay.py's per-file module names) does not register the ops twice.
 
 Op names follow the reference (library/rmsnorm.py:86-103, geglu.py:85-101,
 relpos_attention.py:175-195): krsi::rmsnorm_fwd/bwd, krsi::geglu_fwd/bwd,
-krsi::relpos_attn_fwd/bwd. Their schemas are internal to this library.
+krsi::relpos_attn_fwd/bwd; krsi::relpos_bucket_gather/sum (the T5 table step) have
+no counterpart there. Their schemas are internal to this library.
 """
 from __future__ import annotations
 
@@ -123,3 +124,39 @@ def _relpos_backward(ctx, dout, _d32, _dlse):
 
 
 relpos_fwd_op.register_autograd(_relpos_backward, setup_context=_relpos_setup)
+
+# ------------------------------------------ bucketed relative-position table
+
+
+@torch.library.custom_op("krsi::relpos_bucket_gather", mutates_args=())
+def bucket_gather_op(table: Tensor, bucket: Tensor, S: int) -> Tensor:
+    return _hip.relpos_bucket_gather(table, bucket, S)
+
+
+@bucket_gather_op.register_fake
+def _(table, bucket, S):
+    return table.new_empty((table.shape[1], 2 * S - 1))
+
+
+@torch.library.custom_op("krsi::relpos_bucket_sum", mutates_args=())
+def bucket_sum_op(dpd: Tensor, bucket: Tensor, S: int, num_buckets: int) -> Tensor:
+    return _hip.relpos_bucket_sum(dpd, bucket, S, num_buckets)
+
+
+@bucket_sum_op.register_fake
+def _(dpd, bucket, S, num_buckets):
+    return dpd.new_empty((num_buckets, dpd.shape[0]))
+
+
+def _bucket_setup(ctx, inputs, output):
+    table, bucket, S = inputs
+    ctx.save_for_backward(bucket)
+    ctx.S, ctx.nb = S, table.shape[0]
+
+
+def _bucket_backward(ctx, dpd):
+    (bucket,) = ctx.saved_tensors
+    return bucket_sum_op(dpd.contiguous(), bucket, ctx.S, ctx.nb), None, None
+
+
+bucket_gather_op.register_autograd(_bucket_backward, setup_context=_bucket_setup)

@@ -10,6 +10,7 @@ Backward keeps an fp32 copy of O for delta = rowsum(dO * O). No causal mask; D %
 (so D = 72 runs too). Drop-in for the reference's library/relpos_attention.py (same functions and
 arguments; relpos_attention.py:198-222).
 """
+import math
 import sys
 from pathlib import Path
 
@@ -48,6 +49,66 @@ def relpos_attention(qkv, pd, B, S, H, D, scale):
     if compiling():
         return _ops().relpos_fwd_op(qkv, pd, B, S, H, D, scale)[0]
     return RelPosAttention.apply(qkv, pd, B, S, H, D, scale)
+
+
+# ------------------------------------------ bucketed relative-position table (T5)
+_BUCKETS = {}
+
+
+def t5_relative_position_bucket(S, bidirectional=True, num_buckets=32, max_distance=128, device="cuda"):
+    """[2S-1] int32: the T5 bucket of every distance d = j - i = r - (S - 1) (memory minus query
+    position), by the T5 formula (transformers T5Attention._relative_position_bucket) in the
+    same fp32 op sequence, so distances on a bucket boundary fall as they do in T5. Index setup
+    only (built once per arguments and device, then cached); the table math is in the kernels."""
+    if compiling():  # traced into the graph (no cache mutation under torch.compile)
+        return _t5_bucket_map(S, bidirectional, num_buckets, max_distance, device)
+    key = (S, bool(bidirectional), num_buckets, max_distance, str(device))
+    if key not in _BUCKETS:
+        _BUCKETS[key] = _t5_bucket_map(S, bidirectional, num_buckets, max_distance, device)
+    return _BUCKETS[key]
+
+
+def _t5_bucket_map(S, bidirectional, num_buckets, max_distance, device):
+    d = torch.arange(2 * S - 1, device=device, dtype=torch.long) - (S - 1)
+    ret = torch.zeros_like(d)
+    n = num_buckets
+    if bidirectional:
+        n //= 2
+        ret = ret + (d > 0).to(torch.long) * n
+        a = torch.abs(d)
+    else:
+        a = -torch.min(d, torch.zeros_like(d))
+    max_exact = n // 2
+    large = max_exact + (torch.log(a.float() / max_exact) / math.log(max_distance / max_exact)
+                         * (n - max_exact)).to(torch.long)
+    large = torch.min(large, torch.full_like(large, n - 1))
+    return (ret + torch.where(a < max_exact, a, large)).to(torch.int32)
+
+
+class BucketTable(torch.autograd.Function):
+    """pd [H, 2S-1] = table[bucket, :].T by the gather kernel; backward: the bucket-sum kernel
+    (the reference's note LESSONS.md:35: diagonals, then buckets, no scatter)."""
+
+    @staticmethod
+    def forward(ctx, table, bucket, S):
+        ctx.save_for_backward(bucket)
+        ctx.S, ctx.nb = S, table.shape[0]
+        return _hip.relpos_bucket_gather(table, bucket, S)
+
+    @staticmethod
+    def backward(ctx, dpd):
+        (bucket,) = ctx.saved_tensors
+        return _hip.relpos_bucket_sum(dpd, bucket, ctx.S, ctx.nb), None, None
+
+
+def t5_relpos_table(table, S, bidirectional=True, max_distance=128):
+    """pd [H, 2S-1] fp32 for relpos_attention from a T5 relative_attention_bias weight
+    table [num_buckets, H] fp32: pd[h, j - i + S - 1] = table[bucket(j - i), h], the bias
+    T5Attention.compute_bias builds as [1, H, S, S]. Differentiable w.r.t. table."""
+    bucket = t5_relative_position_bucket(S, bidirectional, table.shape[0], max_distance, table.device)
+    if compiling():
+        return _ops().bucket_gather_op(table, bucket, S)
+    return BucketTable.apply(table, bucket, S)
 
 
 def reference(qkv, pd, B, S, H, D, scale):

@@ -277,6 +277,16 @@ def relpos_kernel_emulated(qkv, pd, B, S, H, D, scale, dout, dtype=torch.bfloat1
     return out, dqkv.to(dtype), dpd
 
 
+def t5_bucket(S: int, bidirectional: bool = True, num_buckets: int = 32, max_distance: int = 128):
+    """[2S-1] int64 T5 bucket of every distance j - i = r - (S - 1), by transformers'
+    T5Attention._relative_position_bucket itself (the published implementation the T5 bias
+    step follows; transformers is installed, this runs it on the CPU as the checker)."""
+    from transformers.models.t5.modeling_t5 import T5Attention  # noqa: PLC0415
+
+    d = torch.arange(2 * S - 1, dtype=torch.long) - (S - 1)
+    return T5Attention._relative_position_bucket(d, bidirectional, num_buckets, max_distance)
+
+
 def relpos_np64(qkv: np.ndarray, pd: np.ndarray, B, S, H, D, scale, dout: np.ndarray):
     """Float64 closed form with explicit loops over (b, h):
       s = q k^T scale + T, p = softmax(s), o = p v, lse = log2 sum exp(s)

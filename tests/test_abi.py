@@ -123,6 +123,17 @@ def test_dtype_argument_validated_before_launch():
     assert _hip.DTYPE_CODES == {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
+def test_bucket_entry_points_validate_before_launch():
+    lib = _hip.lib()
+    SHAPE, NULLP = 2, 1
+    assert lib.krsi_relpos_bucket_gather(FAKE, FAKE, FAKE, 0, 4, 32, NULL) == SHAPE
+    assert lib.krsi_relpos_bucket_gather(FAKE, FAKE, FAKE, 16, 0, 32, NULL) == SHAPE
+    assert lib.krsi_relpos_bucket_gather(FAKE, FAKE, FAKE, 16, 4, 0, NULL) == SHAPE
+    assert lib.krsi_relpos_bucket_gather(NULL, FAKE, FAKE, 16, 4, 32, NULL) == NULLP
+    assert lib.krsi_relpos_bucket_sum(FAKE, NULL, FAKE, 16, 4, 32, NULL) == NULLP
+    assert lib.krsi_relpos_bucket_sum(FAKE, FAKE, FAKE, 16, 70000, 32, NULL) == SHAPE
+
+
 def test_python_layer_has_no_cpu_path():
     import geglu
     import relpos_attention

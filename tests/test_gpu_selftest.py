@@ -45,3 +45,40 @@ def test_relpos_selftest_protocol_and_compile():
     pd = seeded((H, 2 * S - 1), 1, dtype=torch.float32)
     _check(selftest_autograd(lambda q, p: A.relpos_attention(q, p, B, S, H, D, 1.0),
                              lambda q, p: A.reference(q, p, B, S, H, D, 1.0), [qkv, pd], time=False))
+
+
+def test_t5_table_chain_selftest_protocol_and_compile():
+    """T5 relative_attention_bias table -> pd (gather kernel) -> attention, gradient to the table
+    through the bucket-sum kernel, against the reference with pd gathered by torch indexing."""
+    B, S, H, D = 2, 256, 4, 64
+    log(f"selftest_autograd t5 table chain B{B} S{S} H{H} D{D} + torch.compile(fullgraph)")
+    torch.manual_seed(0)
+    qkv = (0.6 * seeded((B * S, 3 * H * D), 0, dtype=torch.float32)).to(torch.bfloat16)
+    table = seeded((32, H), 2, std=0.5, dtype=torch.float32)
+    bucket = A.t5_relative_position_bucket(S, True, 32, 128, "cuda").long()
+    _check(selftest_autograd(lambda q, t: A.relpos_attention(q, A.t5_relpos_table(t, S), B, S, H, D, 0.125),
+                             lambda q, t: A.reference(q, t[bucket].t(), B, S, H, D, 0.125),
+                             [qkv, table], time=False))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_rmsnorm_geglu_selftest_other_dtypes(dt):
+    log(f"selftest_autograd rmsnorm and geglu in {dt} + torch.compile(fullgraph)")
+    torch.manual_seed(0)
+    x = seeded((512, 1152), 0, dtype=dt)
+    w = (1 + 0.02 * seeded((1152,), 1, dtype=torch.float32)).to(dt)
+    _check(selftest_autograd(lambda x, w: R.rmsnorm(x, w, 1e-6), lambda x, w: R.reference(x, w, 1e-6),
+                             [x, w], time=False))
+    u = seeded((256, 2 * 1408), 3, dtype=dt)
+    _check(selftest_autograd(lambda u: G.geglu(u, approximate="tanh"),
+                             lambda u: G.reference(u, approximate="tanh"), [u], time=False))
+
+
+def test_relpos_selftest_fp16():
+    B, S, H, D = 2, 256, 4, 64
+    log(f"selftest_autograd relpos fp16 B{B} S{S} H{H} D{D} + torch.compile(fullgraph)")
+    torch.manual_seed(0)
+    qkv = (0.6 * seeded((B * S, 3 * H * D), 0, dtype=torch.float32)).to(torch.float16)
+    pd = seeded((H, 2 * S - 1), 1, dtype=torch.float32)
+    _check(selftest_autograd(lambda q, p: A.relpos_attention(q, p, B, S, H, D, 1.0),
+                             lambda q, p: A.reference(q, p, B, S, H, D, 1.0), [qkv, pd], time=False))

@@ -285,3 +285,35 @@ def test_kernel_emulation_fp16_is_close_to_fp32():
     assert k[0].dtype == torch.float16
     for a, b in ((k[0], r[0]), (k[1], r[2]), (k[2], r[3])):
         assert ((a.float() - b).norm() / b.norm()) < 5e-3
+
+
+# -------------------------------------------------------- T5 bucket map (host side)
+@pytest.mark.parametrize("S,bidir,nb,maxd", [(1, True, 32, 128), (2, True, 32, 128), (100, True, 32, 128),
+                                             (4096, True, 32, 128), (4096, False, 32, 128),
+                                             (1000, True, 64, 256), (300, True, 16, 32)])
+def test_t5_bucket_map_matches_transformers(S, bidir, nb, maxd):
+    """The library's bucket map (torch ops, any device; here the CPU) equals transformers'
+    T5Attention._relative_position_bucket for every distance, boundary distances included."""
+    import relpos_attention as A
+
+    ours = A.t5_relative_position_bucket(S, bidir, nb, maxd, "cpu")
+    assert ours.dtype == torch.int32
+    assert torch.equal(ours.long(), O.t5_bucket(S, bidir, nb, maxd))
+
+
+def test_t5_bucket_map_against_closed_form():
+    """The T5 map from its definition in float64 away from bucket boundaries: distance 0 -> 0,
+    |d| < 8 exact, sign split at 16, |d| >= 128 -> last bucket, log spacing in between."""
+    b = O.t5_bucket(4096).numpy()
+    d = np.arange(-4095, 4096)
+    for dist, bk in zip(d, b):
+        a = abs(int(dist))
+        base = 16 if dist > 0 else 0
+        if a < 8:
+            want = a
+        else:
+            x = 8 + math.log(a / 8) / math.log(16) * 8
+            if abs(x - round(x)) < 1e-6:       # on a boundary: fp32 rounding decides
+                continue
+            want = min(int(x), 15)
+        assert bk == base + want, (dist, bk, base + want)
