@@ -384,8 +384,11 @@ int pick_vpt(int nch, int wpr) {
 // registers per lane, more waves in flight.
 int pick_wpr(int nch) { return nch <= 256 ? 1 : 4; }
 // The backward holds w, its dw share and two rows of g and x per lane, so it
-// spreads a row over more waves: at most 2 chunks per lane up to 512 chunks.
-int pick_wpr_bwd(int nch) { return nch <= 128 ? 1 : (nch <= 256 ? 2 : 4); }
+// spreads a row over more waves: 2 waves per row up to 512 chunks (4 chunks per
+// lane, occupancy 2: at [32768, 4096] bf16 123 us against 136 us with 4 waves
+// per row and 2 chunks per lane, whose per-row barrier then costs more than the
+// registers save), 4 beyond.
+int pick_wpr_bwd(int nch) { return nch <= 128 ? 1 : (nch <= 512 ? 2 : 4); }
 
 // Rows per block of the scalar dw kernel: at least kScalarRowChunk, and few
 // enough blocks that the partials stay within kBwdMaxBlocks rows.
@@ -457,7 +460,7 @@ int rmsnorm_bwd(const void* g, const void* x, const void* w, const float* rstd, 
     done = true;                                                           \
   }
     KRSI_BWD_CASE(1, 1) KRSI_BWD_CASE(1, 2) KRSI_BWD_CASE(2, 1) KRSI_BWD_CASE(2, 2)
-    KRSI_BWD_CASE(4, 1) KRSI_BWD_CASE(4, 2) KRSI_BWD_CASE(4, 4) KRSI_BWD_CASE(4, 8)
+    KRSI_BWD_CASE(2, 4) KRSI_BWD_CASE(4, 2) KRSI_BWD_CASE(4, 4) KRSI_BWD_CASE(4, 8)
 #undef KRSI_BWD_CASE
   }
   if (!done) {
