@@ -70,3 +70,13 @@ def test_geglu_rejects_bad_input():
         G.geglu(torch.randn(4, 7, device="cuda", dtype=torch.bfloat16))  # odd width
     with pytest.raises(ValueError):
         G.geglu(torch.randn(4, 8, device="cuda", dtype=torch.bfloat16), approximate="sigmoid")
+
+
+@pytest.mark.parametrize("f", [8, 3])
+def test_geglu_rows_beyond_grid_y(f):
+    """rows > 65535: the grid's row dimension is capped and each block strides over rows."""
+    log(f"geglu rows=70000 f={f}")
+    u = seeded((70000, 2 * f), 70 + f, std=2.0)
+    g = seeded((70000, f), 71)
+    ref32, orig, cand = _run(u, g, "tanh")
+    assert_parity(["out", "du"], ref32, orig, cand)

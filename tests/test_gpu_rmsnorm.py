@@ -100,3 +100,15 @@ def test_rmsnorm_rejects_cpu_and_wrong_dtype():
     with pytest.raises(TypeError):  # float64 is not an activation dtype of the kernels
         R.rmsnorm(torch.randn(4, 8, device="cuda", dtype=torch.float64),
                   torch.ones(8, device="cuda", dtype=torch.float64), EPS)
+
+
+@pytest.mark.parametrize("n", [64, 6])
+def test_rmsnorm_many_short_rows(n):
+    """100000 rows: the forward grid is large and the persistent backward loops ~49 times per
+    row group (vector path at n = 64, scalar path at n = 6)."""
+    log(f"rmsnorm rows=100000 n={n}")
+    x = seeded((100000, n), 72 + n)
+    w = seeded((n,), 73, std=0.1, mean=1.0)
+    g = seeded((100000, n), 74)
+    ref32, orig, cand = _run(x, w, g)
+    assert_parity(["y", "dx", "dw"], ref32, orig, cand)
