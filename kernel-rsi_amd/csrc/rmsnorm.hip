@@ -157,8 +157,10 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
   const int64_t groups_total = (int64_t)gridDim.x * RPB;
   const int64_t iters = (rows + groups_total - 1) / groups_total;
   // The next row's g, x and rstd are requested before this row is reduced and written, so
-  // every wave keeps one row of loads in flight. x and dx take non-temporal loads and stores
-  // (measured best: also marking g non-temporal was slower, 141 vs 133 us at [32768, 4096]).
+  // every wave keeps one row of loads in flight. g, x and dx take non-temporal loads and
+  // stores: at [32768, 4096] a forward + backward step takes 211 us against 215 us with g
+  // loaded normally (the backward alone is slower, 137 vs 123 us, but leaves more of x in the
+  // memory-side cache for the next forward; marking the forward's x loads as well: 222 us).
   u32x4 gv[VPT], xv[VPT];
   float r;
   auto fetch = [&](int64_t row, u32x4* gq, u32x4* xq, float& rq) {
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(
     for (int k = 0; k < VPT; ++k) {
       const int c = gtid + k * GT;
       const bool ok = live && c < nch;
-      gq[k] = ok ? gr[c] : u32x4{0u, 0u, 0u, 0u};
+      gq[k] = ok ? __builtin_nontemporal_load(&gr[c]) : u32x4{0u, 0u, 0u, 0u};
       xq[k] = ok ? __builtin_nontemporal_load(&xr[c]) : u32x4{0u, 0u, 0u, 0u};
     }
     rq = live ? rstd[row] : 0.f;
