@@ -991,14 +991,23 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
   const int npd = 2 * S - 1;
   const int RS = S + rows;
   const int rlen = S + rows - 1;
+  // Terms e = wave, wave + 4, ... are loaded 16 at a time (all requests in flight together:
+  // the kernel is latency-bound otherwise) and added in e order; absent terms add 0.
+  constexpr int kBatch = 16;
   float acc = 0.f;
   if (k < npd) {
     const int terms = B * nqb;
-#pragma unroll 4
-    for (int e = wave; e < terms; e += 4) {
-      const int b = e / nqb, kb = e - b * nqb;
-      const int r = k - rows * kb;
-      if (r >= 0 && r < rlen) acc += part[((int64_t)(b * H + h) * nqb + kb) * RS + r];
+    for (int e0 = wave; e0 < terms; e0 += 4 * kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + 4 * i;
+        const int b = e / nqb, kb = e - b * nqb;
+        const int r = k - rows * kb;
+        v[i] = (e < terms && r >= 0 && r < rlen) ? part[((int64_t)(b * H + h) * nqb + kb) * RS + r] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) acc += v[i];
     }
   }
   s[wave][lane] = acc;
