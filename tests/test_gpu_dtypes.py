@@ -164,3 +164,10 @@ def test_relpos_fp32_rejected():
     pd = torch.zeros(2, 7, device="cuda", dtype=torch.float32)
     with pytest.raises(TypeError):
         A.relpos_attention(qkv, pd, 2, 4, 2, 16, 0.25)
+
+
+def test_relpos_fp16_config5_shape():
+    """The BASELINE config 5 shape in fp16 (B4 H16 L4096 D64), against the fp32 reference on the
+    GPU, with the same two criteria as the small cases."""
+    log("relpos fp16 B4 S4096 H16 D64")
+    _relpos_fp16(4, 4096, 16, 64, 1 / 8, ref_device="cuda")
