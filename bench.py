@@ -3,7 +3,7 @@
 fwd+bwd and TFLOP/s of relative-position flash attention fwd+bwd, each as a fraction of the
 MI355X roofline, with the reference's eager torch path timed on the host CPU beside it.
 
-    python bench.py [--steps K] [--warmup W] [--only relpos,rmsnorm,geglu,relpos_fwd] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--only relpos,rmsnorm,geglu,relpos_fwd,relpos_fp16] [--no-cpu]
 
 A "step" is one forward + backward pass of a kernel over one batch of synthetic input that
 is already resident in HBM (3 and 5; config 4 is the forward-only
@@ -170,12 +170,13 @@ def bench_geglu(args, approximate="none") -> dict:
     return res
 
 
-def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False) -> dict:
+def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False, dtype=torch.bfloat16) -> dict:
     import _hip
     scale = 1.0 / math.sqrt(D)
-    qkv = _gen((B * S, 3 * H * D), 0).cuda()
+    qkv = _gen((B * S, 3 * H * D), 0, dtype=dtype).cuda()
     pd = _gen((H, 2 * S - 1), 1, std=0.02, dtype=torch.float32).cuda()
-    dout = _gen((B * S, H * D), 2).cuda()
+    dout = _gen((B * S, H * D), 2, dtype=dtype).cuda()
+    dname = "bf16" if dtype == torch.bfloat16 else "fp16"
     st = torch.cuda.current_stream()
     fl_fwd = 4 * B * H * S * S * D
     fl_bwd = 10 * B * H * S * S * D
@@ -198,8 +199,9 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False) -> dict:
                      args.steps, args.warmup, st)
     total = fl_fwd + fl_bwd
     tfl = total / (t["ms_mean"] * 1e-3) / 1e12
-    res = {"workload": f"relpos attention fwd+bwd B{B} H{H} L{S} D{D} bf16, pd fp32 [H,2L-1] "
-                       "(BASELINE config 5)", "value": round(tfl, 2), "unit": "TFLOP/s",
+    res = {"workload": f"relpos attention fwd+bwd B{B} H{H} L{S} D{D} {dname}, pd fp32 [H,2L-1] "
+                       "(BASELINE config 5" + (")" if dname == "bf16" else " shape, fp16 activations)"),
+           "value": round(tfl, 2), "unit": "TFLOP/s",
            "ms_per_step": round(t["ms_mean"], 4), "algorithmic_flops": total,
            "kernels": {"relpos_fwd": {"ms": round(tf["ms_mean"], 4), "flops": fl_fwd,
                                       "TFLOP/s": round(fl_fwd / tf["ms_mean"] / 1e9, 1)},
@@ -210,7 +212,7 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False) -> dict:
                         "frac": round(tfl / PEAK_BF16_TFLOPS, 4), "traffic": None,
                         "scope": "one fwd+bwd step = relpos_fwd_kernel + relpos_bwd_dq_kernel + "
                                  "relpos_bwd_dkdv_kernel + relpos_dpd_reduce, 14*B*H*L^2*D flops"}}
-    if not args.no_cpu:
+    if not args.no_cpu and dname == "bf16":
         import krsi_oracle as O
         nb = 2  # bounded sample: 2 of the B*H = 64 (batch, head) pairs, full L
         qs = qkv.view(B, S, 3, H, D)[0, :, :, :nb].reshape(S, 3 * nb * D).cpu()
@@ -279,7 +281,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="relpos,relpos_fwd,rmsnorm,geglu")
+    ap.add_argument("--only", default="relpos,relpos_fwd,rmsnorm,geglu,relpos_fp16")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -296,6 +298,8 @@ def main() -> None:
         comps["relpos_attention"] = bench_relpos(args)
     if "relpos_fwd" in only:
         comps["relpos_attention_fwd_config4"] = bench_relpos(args, B=2, S=1024, H=16, D=72, fwd_only=True)
+    if "relpos_fp16" in only:
+        comps["relpos_attention_fp16"] = bench_relpos(args, dtype=torch.float16)
     if "rmsnorm" in only:
         comps["rmsnorm"] = bench_rmsnorm(args)
     if "geglu" in only:
