@@ -237,12 +237,14 @@ struct Dma {
   static_assert(NCHV % 64 == 0, "a wave fills whole 64-chunk runs");
 };
 
+// tid: the thread's index within the NT threads that share the tile (threadIdx.x unless a
+// workgroup stages several tiles with separate thread groups).
 template <int DP, int NT>
-__device__ __forceinline__ void dma_offsets(uint32_t* voff, int64_t ld, int D) {
+__device__ __forceinline__ void dma_offsets(uint32_t* voff, int64_t ld, int D, int tid) {
   constexpr int C = Dma<DP, NT>::C;
 #pragma unroll
   for (int k = 0; k < Dma<DP, NT>::GPT; ++k) {
-    const int p = min(k * NT + (int)threadIdx.x, Dma<DP, NT>::NCHV - 1);  // past the tile: unused
+    const int p = min(k * NT + tid, Dma<DP, NT>::NCHV - 1);  // past the tile: unused
     const int row = p / C;
     const int j = (p - row * C) ^ swz<Geo<DP>::DPV>(row);
     voff[k] = opaque(8 * j < D ? (uint32_t)(row * ld + 8 * j) * 2u : kOob);
@@ -262,14 +264,24 @@ __device__ __forceinline__ void dma16(rsrc_t r, uint32_t voff, uint32_t m0) {
 // Rows p0..p0+63 of the [S, D] slice whose row 0 is `origin` (row stride ld) into the
 // staged tile at `tile`, asynchronously (vmcnt): wait and barrier before reading it.
 template <int DP, int NT>
+__device__ __forceinline__ void dma_offsets(uint32_t* voff, int64_t ld, int D) {
+  dma_offsets<DP, NT>(voff, ld, D, (int)threadIdx.x);
+}
+
+// w: the wave's index within the thread group (wave-uniform).
+template <int DP, int NT>
 __device__ __forceinline__ void dma_tile(uint16_t* tile, const uint32_t* voff, const uint16_t* origin,
-                                         int64_t ld, int p0, int S, int D) {
+                                         int64_t ld, int p0, int S, int D, int w) {
   const rsrc_t r = make_rsrc(origin + (int64_t)p0 * ld, (uint32_t)(((int64_t)(S - 1 - p0) * ld + D) * 2));
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
   for (int k = 0; k < Dma<DP, NT>::GPT; ++k)
     if (Dma<DP, NT>::NCHV % NT == 0 || k * NT + 64 * w < Dma<DP, NT>::NCHV)
       dma16(r, voff[k], (uint32_t)(uintptr_t)(lds_void*)(tile + (k * NT + 64 * w) * 8));
+}
+template <int DP, int NT>
+__device__ __forceinline__ void dma_tile(uint16_t* tile, const uint32_t* voff, const uint16_t* origin,
+                                         int64_t ld, int p0, int S, int D) {
+  dma_tile<DP, NT>(tile, voff, origin, ld, p0, S, D, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
 }
 
 // Wait for this thread's outstanding loads (the tile DMA among them) and LDS operations,
@@ -285,12 +297,14 @@ __device__ __forceinline__ void drain_and_sync() {
 // one step ahead and scaled only when stashed, so nothing waits on the load (or on
 // the tile DMA issued next to it) before the step that consumes it.
 template <int NW>
-__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn) {
+__device__ __forceinline__ void load_bias(float* regs, const float* pdh, int npd, int wb, int sgn,
+                                          int tid = -1) {
   using K = Blk<NW>;
   const rsrc_t r = make_rsrc(pdh, (uint32_t)npd * 4u);
+  if (tid < 0) tid = threadIdx.x;
 #pragma unroll
   for (int k = 0; k < K::BPT; ++k) {
-    const int x = threadIdx.x + k * K::NT;
+    const int x = tid + k * K::NT;
     regs[k] = bload4(r, opaque(x < K::WIN ? (uint32_t)(wb + sgn * x) * 4u : kOob));
   }
 }
@@ -302,11 +316,12 @@ template <int NW>
 __device__ __forceinline__ constexpr int copy_base(int cc) { return cc == 0 ? 4 : cc * Blk<NW>::WLD; }
 
 template <int NW>
-__device__ __forceinline__ void stash_bias(const float* regs, float* bw, float bmul) {
+__device__ __forceinline__ void stash_bias(const float* regs, float* bw, float bmul, int tid = -1) {
   using K = Blk<NW>;
+  if (tid < 0) tid = threadIdx.x;
 #pragma unroll
   for (int k = 0; k < K::BPT; ++k) {
-    const int x = threadIdx.x + k * K::NT;
+    const int x = tid + k * K::NT;
     if (x < K::WIN) {
       const float v = regs[k] * bmul;
 #pragma unroll
@@ -547,6 +562,149 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
 
   fwd_store<DT, DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
                 lse + (int64_t)bh * S + qi);
+}
+
+// ------------------------------------------- forward, keys split inside the workgroup
+// For grids too small to give every SIMD more than one wave (fewer than two workgroups of
+// relpos_fwd_kernel per CU): a workgroup of 8 waves owns the same 128 queries; waves 0-3
+// stream key steps [0, T - T1) and waves 4-7 steps [T - T1, T), T1 = ceil(T / 2), each group
+// with its own staged tiles and bias windows and the same step code as relpos_fwd_kernel.
+// Both groups pass the same T1 barriers (group 0 idles in its last iteration when T is odd);
+// only group 1's last step can be partial, and it runs in the last iteration. At
+// the end group 1 hands its running max, row sum and accumulators to group 0 through LDS,
+// which merges them: m = max(m0, m1), x = x0 2^(m0 - m) + x1 2^(m1 - m) for l and O. Each
+// half keeps its own exact running max, so p of the second half is rounded relative to that
+// half's maximum rather than to the running maximum over all earlier keys.
+template <int DT, int DP>
+__global__ __launch_bounds__(512, (DP == 64 ? 4 : 2)) void relpos_fwd_ks_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
+    int D, Fold f) {
+  constexpr int NW = 4;  // waves per key group
+  using G = Geo<DP>;
+  using K = Blk<NW>;
+  constexpr int TILE = kStep * G::DPV;
+  constexpr int BWIN = 4 * K::WLD;
+  constexpr int GRP_HALVES = 2 * TILE;  // one group's double-buffered tile, in uint16
+  // K tiles of both groups, then V tiles of both groups; reused for the hand-over at the end.
+  __shared__ __attribute__((aligned(16))) uint16_t stage[4 * GRP_HALVES];
+  __shared__ __attribute__((aligned(16))) float Bw[2 * 2 * BWIN];
+  uint16_t* const Ks = stage;
+  uint16_t* const Vs = stage + 2 * GRP_HALVES;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
+  const int grp = __builtin_amdgcn_readfirstlane(wave >> 2);
+  const int gw = __builtin_amdgcn_readfirstlane(wave & 3);  // wave within the group
+  const int gtid = threadIdx.x & (K::NT - 1);
+  TileLane<DP> L;
+  L.init(lane);
+  const int nqb = (S + K::ROWS - 1) / K::ROWS;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int bh = tile / nqb, b = bh / H, h = bh - b * H;
+  const int qb = tile - bh * nqb;
+  const int i_wg = qb * K::ROWS;
+  const int ii = gw * 32 + l32;
+  const int qi = i_wg + ii;
+  const bool qvalid = qi < S;
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t HD = (int64_t)H * D;
+  const uint16_t* q0 = qkv + tok0 * ld + (int64_t)h * D;
+  const uint16_t* k0p = q0 + HD;
+  const uint16_t* v0p = q0 + 2 * HD;
+  const int npd = 2 * S - 1;
+  const float* pdh = pd + (int64_t)h * npd;
+  const float c = f.c;
+  uint16_t* Kg = Ks + grp * GRP_HALVES;
+  uint16_t* Vg = Vs + grp * GRP_HALVES;
+  float* Bg = Bw + grp * 2 * BWIN;
+
+  u32x4 qreg[G::KS];
+#pragma unroll
+  for (int s = 0; s < G::KS; ++s) {
+    const int d0 = 16 * s + 8 * g;
+    qreg[s] = (qvalid && d0 < D) ? fold_operand(ld16(q0 + (int64_t)qi * ld + d0), f) : kZero4;
+  }
+  f32x16 oacc[G::DB];
+#pragma unroll
+  for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_run = -INFINITY, l_run[2] = {0.f, 0.f};
+
+  uint32_t voff[Dma<DP, K::NT>::GPT];
+  dma_offsets<DP, K::NT>(voff, ld, D, gtid);
+  float bst[K::BPT];
+  const int T = (S + kStep - 1) / kStep;
+  const int T1 = (T + 1) / 2;
+  const int tbeg = grp == 0 ? 0 : T - T1;      // this group's first step
+  const int tend = grp == 0 ? T - T1 : T;      // one past its last
+  const int wb0 = S - 1 - i_wg - (K::ROWS - 1);
+  if (tbeg < tend) {
+    dma_tile<DP, K::NT>(Kg, voff, k0p, ld, tbeg * kStep, S, D, gw);
+    dma_tile<DP, K::NT>(Vg, voff, v0p, ld, tbeg * kStep, S, D, gw);
+    load_bias<NW>(bst, pdh, npd, wb0 + tbeg * kStep, 1, gtid);
+  }
+
+  // Iteration it handles step tbeg + it of this group from buffer it & 1 (requested one
+  // iteration earlier); the barrier (shared by both groups) publishes it and retires every
+  // wave's reads of the other buffer.
+  auto step = [&](int it, auto buf, auto tail) {
+    constexpr int B = decltype(buf)::value;
+    const int t = tbeg + it;
+    const bool live = t < tend;
+    if (live) stash_bias<NW>(bst, Bg + B * BWIN, f.bmul, gtid);
+    drain_and_sync();
+    if (t + 1 < tend) {
+      const int j1 = (t + 1) * kStep;
+      dma_tile<DP, K::NT>(Kg + (1 - B) * TILE, voff, k0p, ld, j1, S, D, gw);
+      dma_tile<DP, K::NT>(Vg + (1 - B) * TILE, voff, v0p, ld, j1, S, D, gw);
+      load_bias<NW>(bst, pdh, npd, wb0 + j1, 1, gtid);
+    }
+    if (live)
+      fwd_step<DT, DP, NW, decltype(tail)::value>(Kg + B * TILE, Vg + B * TILE, Bg + B * BWIN, L, qreg,
+                                                  oacc, m_run, l_run, t * kStep, S, ii, g, c);
+  };
+  // Every step before the last iteration is full; the last may hold group 1's partial step.
+  int it = 0;
+  for (; it + 2 < T1; it += 2) {
+    step(it, kBuf0, kFull);
+    step(it + 1, kBuf1, kFull);
+  }
+  if (it + 1 < T1) {
+    step(it, kBuf0, kFull);
+    step(it + 1, kBuf1, kTail);
+  } else {
+    step(it, kBuf0, kTail);
+  }
+
+  // Hand-over through the (now idle) tile buffers: per lane of group 1, m, l and the
+  // accumulators, at [wave-in-group][slot][lane] so every access is one coalesced row.
+  constexpr int SLOTS = 2 + 16 * G::DB;
+  static_assert(4 * SLOTS * 64 * 4 <= (int)sizeof(stage), "the hand-over fits the tile buffers");
+  __syncthreads();
+  float* mine = reinterpret_cast<float*>(stage) + (gw * SLOTS) * 64 + lane;
+  if (grp == 1) {
+    mine[0] = m_run;
+    mine[64] = l_run[0] + l_run[1];
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mine[(2 + 16 * db + r) * 64] = oacc[db][r];
+  }
+  __syncthreads();
+  if (grp == 0) {
+    const float m1 = mine[0], l1 = mine[64];
+    const float m = fmaxf(m_run, m1);
+    const float a0 = __builtin_amdgcn_exp2f(m_run - m);
+    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+    const float lm[2] = {(l_run[0] + l_run[1]) * a0 + l1 * a1, 0.f};
+#pragma unroll
+    for (int db = 0; db < G::DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * a0 + mine[(2 + 16 * db + r) * 64] * a1;
+    fwd_store<DT, DP>(oacc, m, lm, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
+                      lse + (int64_t)bh * S + qi);
+  }
 }
 
 // ------------------------------------------------ backward: delta, dQ and dpd
@@ -1018,6 +1176,9 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
 
 // Waves per workgroup of the three attention kernels.
 constexpr int kFwdNW = 4;
+// Forward grids of fewer workgroups than this (two per CU of the MI355X's 256) split each
+// workgroup's keys over two wave groups (relpos_fwd_ks_kernel).
+constexpr unsigned kFwdSplitBelow = 512;
 constexpr int kDqNW = 4;
 constexpr int kDkdvNW = 4;
 
@@ -1062,6 +1223,11 @@ void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* 
                 int B, int S, int H, int D, Fold f, hipStream_t st) {
   using K = Blk<kFwdNW>;
   const dim3 grid((unsigned)(ceil_div(S, K::ROWS) * B * H));
+  if (grid.x < kFwdSplitBelow && S > kStep) {
+    hipLaunchKernelGGL((relpos_fwd_ks_kernel<DT, DP>), grid, dim3(2 * K::NT), 0, st, (const uint16_t*)qkv,
+                       ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
+    return;
+  }
   hipLaunchKernelGGL((relpos_fwd_kernel<DT, DP, kFwdNW>), grid, dim3(K::NT), 0, st,
                      (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
 }
