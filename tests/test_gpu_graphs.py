@@ -42,28 +42,36 @@ def _replay_matches(fn, inputs, cotangent, other):
         torch.cuda.synchronize()
 
 
-def test_rmsnorm_graph_replay_matches_eager():
-    log("rmsnorm graph replay [2048, 4096]")
-    x, w, gy = seeded((2048, 4096), 0), seeded((4096,), 1, std=0.02, mean=1.0), seeded((2048, 4096), 2)
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=lambda d: str(d).replace("torch.", ""))
+def test_rmsnorm_graph_replay_matches_eager(dt):
+    log(f"rmsnorm graph replay [2048, 4096] {dt}")
+    x = seeded((2048, 4096), 0, dtype=dt)
+    w = seeded((4096,), 1, std=0.02, mean=1.0, dtype=dt)
+    gy = seeded((2048, 4096), 2, dtype=dt)
     other = seeded((512, 1024), 3)
     _replay_matches(lambda a, b: R.rmsnorm(a, b, 1e-6), [x, w], gy,
                     lambda: R.rmsnorm(other, torch.ones(1024, device="cuda", dtype=torch.bfloat16), 1e-6))
 
 
+@pytest.mark.parametrize("dt", DTYPES, ids=lambda d: str(d).replace("torch.", ""))
 @pytest.mark.parametrize("approximate", ["none", "tanh"])
-def test_geglu_graph_replay_matches_eager(approximate):
-    log(f"geglu graph replay [1024, 2*2048] {approximate}")
-    u, gy = seeded((1024, 4096), 4), seeded((1024, 2048), 5)
+def test_geglu_graph_replay_matches_eager(approximate, dt):
+    log(f"geglu graph replay [1024, 2*2048] {approximate} {dt}")
+    u, gy = seeded((1024, 4096), 4, dtype=dt), seeded((1024, 2048), 5, dtype=dt)
     other = seeded((64, 256), 6)
     _replay_matches(lambda a: G.geglu(a, approximate=approximate), [u], gy, lambda: G.geglu(other))
 
 
-def test_t5_table_chain_graph_replay_matches_eager():
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+def test_t5_table_chain_graph_replay_matches_eager(dt):
     B, S, H, D = 1, 256, 4, 64
-    log(f"t5 table + relpos graph replay B{B} S{S} H{H} D{D}")
-    qkv = seeded((B * S, 3 * H * D), 7)
+    log(f"t5 table + relpos graph replay B{B} S{S} H{H} D{D} {dt}")
+    qkv = seeded((B * S, 3 * H * D), 7, dtype=dt)
     table = seeded((32, H), 8, std=0.5, dtype=torch.float32)
-    dout = seeded((B * S, H * D), 9)
+    dout = seeded((B * S, H * D), 9, dtype=dt)
     A.t5_relative_position_bucket(S, True, 32, 128, "cuda")  # build the cached map before capture
     _replay_matches(lambda q, t: A.relpos_attention(q, A.t5_relpos_table(t, S), B, S, H, D, 0.125),
                     [qkv, table], dout, lambda: A.t5_relpos_table(table, 64))
