@@ -133,6 +133,25 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   return v;
 }
 
+// Prologue loads of the register-resident operands. Every lane loads, from p where it has
+// data (ok) and from `safe`, a valid address of the same buffer, where it has none, and the
+// value is then ANDed with an all-ones / zero lane mask. A select of the loaded value (or a
+// conditional load) was turned by the compiler into one branch per load that waited for its
+// data, so the loads of the K steps went to memory one after another; the mask passes
+// through an empty asm, so it cannot be turned back into a select.
+__device__ __forceinline__ uint32_t lane_mask(bool ok) { return opaque(ok ? 0xffffffffu : 0u); }
+__device__ __forceinline__ u32x4 masked(u32x4 v, uint32_t m) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] &= m;
+  return v;
+}
+__device__ __forceinline__ u32x4 ld16_masked(const uint16_t* p, const uint16_t* safe, bool ok, uint32_t m) {
+  return masked(ld16(ok ? p : safe), m);
+}
+__device__ __forceinline__ f32x4 ld16f_masked(const float* p, const float* safe, bool ok, uint32_t m) {
+  return __builtin_bit_cast(f32x4, masked(*reinterpret_cast<const u32x4*>(ok ? p : safe), m));
+}
+
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
 }
@@ -508,7 +527,8 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
 #pragma unroll
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
-    qreg[s] = (qvalid && d0 < D) ? fold_operand(ld16(q0 + (int64_t)qi * ld + d0), f) : kZero4;
+    const bool ok = qvalid && d0 < D;
+    qreg[s] = masked(fold_operand(ld16(ok ? q0 + (int64_t)qi * ld + d0 : q0), f), lane_mask(ok));
   }
 
   f32x16 oacc[G::DB];
@@ -622,7 +642,8 @@ __global__ __launch_bounds__(512, (DP == 64 ? 4 : 2)) void relpos_fwd_ks_kernel(
 #pragma unroll
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
-    qreg[s] = (qvalid && d0 < D) ? fold_operand(ld16(q0 + (int64_t)qi * ld + d0), f) : kZero4;
+    const bool ok = qvalid && d0 < D;
+    qreg[s] = masked(fold_operand(ld16(ok ? q0 + (int64_t)qi * ld + d0 : q0), f), lane_mask(ok));
   }
   f32x16 oacc[G::DB];
 #pragma unroll
@@ -789,18 +810,17 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 3 : DP <= 96 ? 2 : 1)) void re
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
     const bool ok = qvalid && d0 < D;
-    qreg[s] = ok ? fold_operand(ld16(q0 + (int64_t)qi * ld + d0), f) : kZero4;
-    doreg[s] = ok ? ld16(dout + obase + d0) : kZero4;
-    if (ok) {
-      const f32x4 o0 = *reinterpret_cast<const f32x4*>(out32 + obase + d0);
-      const f32x4 o1 = *reinterpret_cast<const f32x4*>(out32 + obase + d0 + 4);
-      float df[8];
-      Elem<DT>::unpack(doreg[s], df);
+    const uint32_t m = lane_mask(ok);
+    qreg[s] = masked(fold_operand(ld16(ok ? q0 + (int64_t)qi * ld + d0 : q0), f), m);
+    doreg[s] = ld16_masked(dout + obase + d0, dout, ok, m);
+    const f32x4 o0 = ld16f_masked(out32 + obase + d0, out32, ok, m);
+    const f32x4 o1 = ld16f_masked(out32 + obase + d0 + 4, out32, ok, m);
+    float df[8];
+    Elem<DT>::unpack(doreg[s], df);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dsum += df[e] * o0[e];
+    for (int e = 0; e < 4; ++e) dsum += df[e] * o0[e];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dsum += df[4 + e] * o1[e];
-    }
+    for (int e = 0; e < 4; ++e) dsum += df[4 + e] * o1[e];
   }
   const float delta = xhalf_sum(dsum);
   // -inf makes p = exp2(acc c - lse) exactly 0 on lanes past S (their acc is finite).
@@ -973,8 +993,9 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
   for (int s = 0; s < G::KS; ++s) {
     const int d0 = 16 * s + 8 * g;
     const bool ok = kvalid && d0 < D;
-    kreg[s] = ok ? fold_operand(ld16(q0 + HD + (int64_t)kj * ld + d0), f) : kZero4;
-    vreg[s] = ok ? ld16(q0 + 2 * HD + (int64_t)kj * ld + d0) : kZero4;
+    const uint32_t m = lane_mask(ok);
+    kreg[s] = masked(fold_operand(ld16(ok ? q0 + HD + (int64_t)kj * ld + d0 : q0), f), m);
+    vreg[s] = ld16_masked(q0 + 2 * HD + (int64_t)kj * ld + d0, q0, ok, m);
   }
 
   f32x16 dk[G::DB], dv[G::DB];
