@@ -1084,8 +1084,20 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
           ds[r] = pv * accp[r];
         }
       }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4 pa = Elem<DT>::pack(&p[8 * u]);
+        const u32x4 dsa = Elem<DT>::pack(&ds[8 * u]);
+#pragma unroll
+        for (int db = 0; db < G::DB; ++db) {
+          dv[db] = mfma32x32x16<DT>(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
+          dk[db] = mfma32x32x16<DT>(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
+        }
+      }
       // dpd: pair p of row group a holds diagonals r_s (register 4a + 2p + 1) and r_s + 1
-      // (register 4a + 2p); the accesses are volatile so they stay in program order.
+      // (register 4a + 2p); the accesses are volatile so they stay in program order. Each
+      // read waits for the write before it (lanes of consecutive pairs share slots), so the
+      // chain comes after the dV/dK products, whose execution it overlaps (-1% backward).
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -1098,16 +1110,6 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
           v.y += ds[4 * a + 2 * pp];
           *rs = v;
         }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const u32x4 pa = Elem<DT>::pack(&p[8 * u]);
-        const u32x4 dsa = Elem<DT>::pack(&ds[8 * u]);
-#pragma unroll
-        for (int db = 0; db < G::DB; ++db) {
-          dv[db] = mfma32x32x16<DT>(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
-          dk[db] = mfma32x32x16<DT>(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
-        }
-      }
       // Diagonals [S + 63 - 64(t-1), S + 126 - 64(t-1)] got their last ds in step t-1 (step
       // t touches [S - 64 - 64t, S + 62 - 64(t-1)], distinct mod 256): fold them into the
       // partial row (r > 0 here), mid-step so the wait overlaps the MFMAs in flight.
