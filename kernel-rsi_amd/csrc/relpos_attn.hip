@@ -1072,20 +1072,26 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
         acc = mfma32x32x16<DT>(row_operand<DP>(Qb, L, qb * 32, s), kreg[s], acc);
         accp = mfma32x32x16<DT>(row_operand<DP>(Ob, L, qb * 32, s), vreg[s], accp);
       }
+      // In two halves u (row groups 2u, 2u + 1): p and ds, the dV/dK products of that half,
+      // then its dpd ring updates. Each ring read waits for the write before it (lanes of
+      // consecutive pairs share slots); placed after the products, the chain overlaps their
+      // execution and the next half's softmax (-1.5% backward against one chain per block).
+      // Ring pair p of row group a holds diagonals r_s (register 4a + 2p + 1) and r_s + 1
+      // (register 4a + 2p); the accesses are volatile so they stay in program order.
       float p[16], ds[16];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const f32x4 nl4 = *reinterpret_cast<const f32x4*>(Lb + qb * 32 + 8 * a + 4 * g);
-#pragma unroll
-        for (int b4 = 0; b4 < 4; ++b4) {
-          const int r = 4 * a + b4;
-          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], c, nl4[b4]));
-          p[r] = pv;
-          ds[r] = pv * accp[r];
-        }
-      }
-#pragma unroll
       for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int a = 2 * u; a < 2 * u + 2; ++a) {
+          const f32x4 nl4 = *reinterpret_cast<const f32x4*>(Lb + qb * 32 + 8 * a + 4 * g);
+#pragma unroll
+          for (int b4 = 0; b4 < 4; ++b4) {
+            const int r = 4 * a + b4;
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[r], c, nl4[b4]));
+            p[r] = pv;
+            ds[r] = pv * accp[r];
+          }
+        }
         const u32x4 pa = Elem<DT>::pack(&p[8 * u]);
         const u32x4 dsa = Elem<DT>::pack(&ds[8 * u]);
 #pragma unroll
@@ -1093,23 +1099,19 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
           dv[db] = mfma32x32x16<DT>(pa, tr_operand<DP>(Ob, L, 2 * qb + u, db), dv[db]);
           dk[db] = mfma32x32x16<DT>(dsa, tr_operand<DP>(Qb, L, 2 * qb + u, db), dk[db]);
         }
+#pragma unroll
+        for (int a = 2 * u; a < 2 * u + 2; ++a)
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp) {
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
+            typedef __attribute__((address_space(3))) f32x2 lds_f32x2;
+            volatile lds_f32x2* rs = (volatile lds_f32x2*)(myring + rp0 - (8 * a + 32 * qb + 2 * pp));
+            f32x2 v = *rs;
+            v.x += ds[4 * a + 2 * pp + 1];
+            v.y += ds[4 * a + 2 * pp];
+            *rs = v;
+          }
       }
-      // dpd: pair p of row group a holds diagonals r_s (register 4a + 2p + 1) and r_s + 1
-      // (register 4a + 2p); the accesses are volatile so they stay in program order. Each
-      // read waits for the write before it (lanes of consecutive pairs share slots), so the
-      // chain comes after the dV/dK products, whose execution it overlaps (-1% backward).
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-          typedef float f32x2 __attribute__((ext_vector_type(2)));
-          typedef __attribute__((address_space(3))) f32x2 lds_f32x2;
-          volatile lds_f32x2* rs = (volatile lds_f32x2*)(myring + rp0 - (8 * a + 32 * qb + 2 * pp));
-          f32x2 v = *rs;
-          v.x += ds[4 * a + 2 * pp + 1];
-          v.y += ds[4 * a + 2 * pp];
-          *rs = v;
-        }
       // Diagonals [S + 63 - 64(t-1), S + 126 - 64(t-1)] got their last ds in step t-1 (step
       // t touches [S - 64 - 64t, S + 62 - 64(t-1)], distinct mod 256): fold them into the
       // partial row (r > 0 here), mid-step so the wait overlaps the MFMAs in flight.
