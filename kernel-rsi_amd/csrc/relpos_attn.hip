@@ -1199,6 +1199,52 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
     dpd[(int64_t)h * npd + k] = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
 }
 
+// The same sum, 4 consecutive diagonals per lane with 128-bit loads, for S % 4 == 0 (then
+// every partial row starts 16-byte aligned and k - rows kb is a multiple of 4). Each
+// diagonal gets the same terms in the same order as in relpos_dpd_reduce, so the result is
+// bitwise the same; entries at or past the row's end (index rlen) are masked to 0.
+__global__ __launch_bounds__(256) void relpos_dpd_reduce4(const float* __restrict__ part,
+                                                          float* __restrict__ dpd, int B, int S,
+                                                          int H, int nqb, int rows) {
+  __shared__ f32x4 s[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int k0 = 4 * (blockIdx.x * 64 + lane);
+  const int h = blockIdx.y;
+  const int npd = 2 * S - 1;
+  const int RS = S + rows;
+  const int rlen = S + rows - 1;
+  constexpr int kBatch = 16;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (k0 < npd) {
+    const int terms = B * nqb;
+    for (int e0 = wave; e0 < terms; e0 += 4 * kBatch) {
+      f32x4 v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int e = e0 + 4 * i;
+        const int b = e / nqb, kb = e - b * nqb;
+        const int r = k0 - rows * kb;
+        v[i] = (e < terms && r >= 0 && r < rlen)
+                   ? *reinterpret_cast<const f32x4*>(part + ((int64_t)(b * H + h) * nqb + kb) * RS + r)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (r + j >= rlen) v[i][j] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) acc += v[i];
+    }
+  }
+  s[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    const f32x4 t = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (k0 + j < npd) dpd[(int64_t)h * npd + k0 + j] = t[j];
+  }
+}
+
 // Waves per workgroup of the three attention kernels.
 constexpr int kFwdNW = 4;
 // Forward grids of fewer workgroups than this (two per CU of the MI355X's 256) split each
@@ -1273,9 +1319,15 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DT, DP, kDkdvNW>), dim3((unsigned)(nkb * B * H)),
                      dim3(KK::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
                      (const float*)delta, (uint16_t*)dqkv, ldd, part, S, H, D, f, scale);
-  const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
-  hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S, H,
-                     nkb, KK::ROWS);
+  if (S % 4 == 0) {
+    const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 256), (unsigned)H);
+    hipLaunchKernelGGL(relpos_dpd_reduce4, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S,
+                       H, nkb, KK::ROWS);
+  } else {
+    const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
+    hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S, H,
+                       nkb, KK::ROWS);
+  }
 }
 
 template <int DT>
