@@ -231,7 +231,7 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False, dtype=torch.bflo
            "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tfl / PEAK_BF16_TFLOPS, 4), "traffic": None,
                         "scope": "one fwd+bwd step = relpos_fwd_kernel + relpos_bwd_dq_kernel + "
-                                 "relpos_bwd_dkdv_kernel + relpos_dpd_reduce, 14*B*H*L^2*D flops"}}
+                                 "relpos_bwd_dkdv_kernel + relpos_dpd_reduce4, 14*B*H*L^2*D flops"}}
     if not args.no_cpu and dname == "bf16":
         import krsi_oracle as O
         nb = 2  # bounded sample: 2 of the B*H = 64 (batch, head) pairs, full L
