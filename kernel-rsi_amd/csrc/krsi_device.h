@@ -20,6 +20,22 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 // bf16 is stored as raw 16-bit patterns. Widening is exact: the bf16 bits are
 // the top half of the fp32 bits.
+// Loads whose lanes may have no data: every lane loads (from a valid address where it has
+// none) and the value is ANDed with an all-ones / zero lane mask. A select of the loaded
+// value, or a conditional load, was turned by the compiler into one branch per load that
+// waited for its data, so consecutive loads went to memory one after another. The mask
+// passes through an empty asm, so the AND cannot be turned back into a select.
+__device__ __forceinline__ uint32_t lane_mask(bool ok) {
+  uint32_t m = ok ? 0xffffffffu : 0u;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+__device__ __forceinline__ u32x4 masked(u32x4 v, uint32_t m) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] &= m;
+  return v;
+}
+
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }

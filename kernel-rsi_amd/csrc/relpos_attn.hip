@@ -133,18 +133,8 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   return v;
 }
 
-// Prologue loads of the register-resident operands. Every lane loads, from p where it has
-// data (ok) and from `safe`, a valid address of the same buffer, where it has none, and the
-// value is then ANDed with an all-ones / zero lane mask. A select of the loaded value (or a
-// conditional load) was turned by the compiler into one branch per load that waited for its
-// data, so the loads of the K steps went to memory one after another; the mask passes
-// through an empty asm, so it cannot be turned back into a select.
-__device__ __forceinline__ uint32_t lane_mask(bool ok) { return opaque(ok ? 0xffffffffu : 0u); }
-__device__ __forceinline__ u32x4 masked(u32x4 v, uint32_t m) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] &= m;
-  return v;
-}
+// Prologue loads of the register-resident operands: every lane loads (from `safe`, a valid
+// address of the same buffer, where it has no data) and masks the value (lane_mask).
 __device__ __forceinline__ u32x4 ld16_masked(const uint16_t* p, const uint16_t* safe, bool ok, uint32_t m) {
   return masked(ld16(ok ? p : safe), m);
 }
