@@ -250,7 +250,7 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False, dtype=torch.bflo
 def _csrc_sha256() -> str:
     import hashlib
     h = hashlib.sha256()
-    for f in sorted((ROOT / "kernel-rsi_amd" / "csrc").glob("*")):
+    for f in sorted((ROOT / "kernel-rsi_amd" / "csrc").glob("*")) + [ROOT / "kernel-rsi_amd" / "build.py"]:
         h.update(f.read_bytes())
     return h.hexdigest()
 
@@ -258,8 +258,8 @@ def _csrc_sha256() -> str:
 def attach_traffic(comps: dict) -> None:
     """roofline.traffic = HBM bytes per step from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     passes (profiles/traffic.json, scaled by a 2 GiB copy). Counters cannot be read inside this
-    process, so the figure is taken from those runs, and only while the kernel sources still hash
-    to what was profiled; otherwise it is null."""
+    process, so the figure is taken from those runs, and only while the kernel sources and the
+    build script (its flags) still hash to what was profiled; otherwise it is null."""
     path = ROOT / "profiles" / "traffic.json"
     try:
         rec = json.loads(path.read_text())
