@@ -1,14 +1,28 @@
 #!/usr/bin/env python3
-"""Benchmark of the fused kernel library on one MI355X: HBM GB/s of RMSNorm and GEGLU
-fwd+bwd and TFLOP/s of relative-position flash attention fwd+bwd, each as a fraction of the
-MI355X roofline, with the reference's eager torch path timed on the host CPU beside it.
+"""Benchmark of the fused kernel library on one MI355X. It reports:
+  * HBM GB/s of RMSNorm and GEGLU fwd+bwd;
+  * TFLOP/s of relative-position flash attention fwd+bwd.
+Each is also given as a fraction of the MI355X roofline. The reference's eager torch path is
+timed on the host CPU beside it.
 
-    python bench.py [--steps K] [--warmup W] [--only relpos,rmsnorm,geglu,relpos_fwd,relpos_fp16] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--only LIST] [--no-cpu] [--cpu-seconds S]
 
-A "step" is one forward + backward pass of a kernel over one batch of synthetic input that
-is already resident in HBM (3 and 5; config 4 is the forward-only
-attention line). Prints ONE JSON line; `value` is the relpos attention fwd+bwd TFLOP/s (the
-dominant kernel), and `components` holds every workload's own figure and roofline.
+LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, rmsnorm, geglu, selftest_shapes,
+config1 (default: all).
+
+A "step" is one forward + backward pass of a kernel over one batch of synthetic input that is
+already resident in HBM (3 and 5; config 4 is the forward-only attention
+line). Prints ONE JSON line. `value` is the relpos attention fwd+bwd TFLOP/s (the dominant
+kernel); `components` holds every workload's own figure and roofline.
+
+Cache-cold protocol: every workload rotates through independent input sets. Their total
+exceeds 3 x (L2 + MALL) = 3 x (32 MB + 256 MB) on an MI355X. Step k runs the forward of set
+k mod n and the backward of set (k - lag) mod n. So between a set's forward and its backward,
+`lag` forwards and backwards of other sets stream several hundred MB through the caches, and
+consecutive steps never touch the same set. This is how a training step sees these kernels:
+the rest of the model runs between a layer's forward and its backward. The per-kernel figures
+rotate the same sets. The old back-to-back figure (forward and backward of one set, over and
+over) is kept as `mall_warm`: it is partly served by the 256 MB MALL and is not the headline.
 """
 from __future__ import annotations
 
@@ -17,6 +31,7 @@ import json
 import math
 import os
 import platform
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -29,16 +44,39 @@ import torch  # noqa: E402
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, published
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
 METRIC = "HBM GB/s (RMSNorm/GEGLU) + TFLOP/s relpos attn fwd+bwd, 1 MI355X"
+CACHE_BYTES = (32 + 256) << 20  # L2 (8 XCDs x 4 MB) + MALL
+# The reference kernels' own fwd+bwd times at its selftest shapes on one H20-3e
+# (library/replay/nvidia_h20_3e.json of the reference), for the selftest-shape lines.
+H20_SELFTEST_US = {"rmsnorm": 39.6, "geglu": 43.7, "relpos_attention": 415.9}
 
 
-def _cpu_model() -> str:
+def cpu_model() -> dict:
+    """What the host CPU says it is: lscpu's model name plus /proc/cpuinfo's family, model and
+    stepping numbers (some VMs report only a generic name such as 'AMD EPYC')."""
+    info = {"model": platform.processor() or "unknown"}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "Model name":
+                info["model"] = val
+            elif key in ("Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)"):
+                info[key] = val
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("cpu family", "model", "stepping", "vendor_id") and key not in info:
+                info[key] = val.strip()
+            if key == "flags":
+                info["avx512f"] = "avx512f" in val.split()
+                break
     except OSError:
         pass
-    return platform.processor() or "unknown"
+    return info
 
 
 def _gen(shape, seed, std=1.0, mean=0.0, dtype=torch.bfloat16):
@@ -50,10 +88,11 @@ _PAD: list = []
 
 
 def _queue_head_start() -> None:
-    """Put ~1.5 ms of unrelated GPU work (fills of a 1 GiB buffer) in the stream, so that the
-    host, whose per-step launch cost (~25-30 us through the Python binding) exceeds the run
-    time of the smallest workload (config 4, ~25 us), enqueues the timed steps before the GPU
-    reaches them and the events see them back to back. The fills run before the first event."""
+    """Put ~1.5 ms of unrelated GPU work (fills of a 1 GiB buffer) in the stream. The host's
+    per-step launch cost (~25-30 us through the Python binding) exceeds the run time of the
+    smallest workloads, so without this head start the GPU would wait for the host. With it,
+    the host enqueues the timed steps before the GPU reaches them, and the events see them back
+    to back. The fills run before the first event."""
     if not _PAD:
         _PAD.append(torch.empty(1 << 28, dtype=torch.float32, device="cuda"))
     for _ in range(10):
@@ -61,14 +100,12 @@ def _queue_head_start() -> None:
 
 
 def _time_steps(step, steps: int, warmup: int, stream: torch.cuda.Stream) -> dict:
-    """Warm up, then time exactly `steps` back-to-back steps bracketed by synchronize, with
-    one pair of HIP events on the stream the kernels launch on around all of them. Returns
-    the mean GPU ms per step (events) and the host's ms per step to enqueue them.
+    """Warm up, then time exactly `steps` back-to-back calls of step(), bracketed by synchronize.
+    One pair of HIP events on the kernels' stream goes around all of them. Returns the mean GPU
+    ms per step (from the events) and the host's ms per step to enqueue them.
 
-    One pair, not one per step: event records between steps leave the GPU idle for ~10 us
-    each (kernel trace: 10-11 us gaps before every step's first kernel, none inside a step
-    or in the untimed warm-up). A/B on one box: the same attention and RMSNorm step times
-    either way (within 1 %), but the 25 us config 4 forward read 27.2 us with a pair per step."""
+    One pair, not one per step: event records between steps leave the GPU idle for ~10 us each
+    (kernel trace: 10-11 us gaps before every step's first kernel)."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -84,12 +121,50 @@ def _time_steps(step, steps: int, warmup: int, stream: torch.cuda.Stream) -> dic
     return {"ms_mean": a.elapsed_time(b) / steps, "host_ms": host}
 
 
-def _cpu_time(fn, min_s: float = 10.0, max_reps: int = 50) -> tuple[float, int]:
-    """Median seconds of fn() after one warm-up, repeating until ~min_s of CPU work."""
+def _rotating(fn, nset: int):
+    """step() calling fn(k mod nset) on its k-th call."""
+    k = [0]
+
+    def step():
+        fn(k[0] % nset)
+        k[0] += 1
+    return step
+
+
+def _pipelined(fwd, bwd, nset: int, lag: int):
+    """step(): the forward of set k mod nset and the backward of set (k - lag) mod nset."""
+    k = [0]
+
+    def step():
+        fwd(k[0] % nset)
+        bwd((k[0] - lag) % nset)
+        k[0] += 1
+    return step
+
+
+def _rate(work: float, ms: float, scale: float) -> float:
+    return work / (ms * 1e-3) / scale
+
+
+def _kernel_line(ms: float, work: int, unit: str) -> dict:
+    key = "bytes" if unit == "GB/s" else "flops"
+    return {"ms": round(ms, 4), key: work, unit: round(_rate(work, ms, 1e9 if unit == "GB/s" else 1e12), 1)}
+
+
+def _roofline(value: float, unit: str) -> dict:
+    peak, bound = (PEAK_HBM_GBS, "hbm") if unit == "GB/s" else (PEAK_BF16_TFLOPS, "mfma")
+    return {"bound": bound, "achieved": round(value, 2), "peak": peak, "unit": unit,
+            "frac": round(value / peak, 4), "traffic": None}
+
+
+# ------------------------------------------------------------------ CPU baseline
+def _cpu_seconds(fn, budget: float, max_reps: int = 50) -> tuple[float, int]:
+    """Median seconds of fn() after one warm-up, repeating until ~budget seconds of work
+    (at least 3 repetitions)."""
     fn()
     times = []
     t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start < min_s or len(times) < 3):
+    while len(times) < max_reps and (time.perf_counter() - t_start < budget or len(times) < 3):
         t = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t)
@@ -105,148 +180,257 @@ def _cpu_threads() -> int:
     return min(n, 16)  # the box's CPU share for one GPU
 
 
+def cpu_legs(kind: str, inputs: dict, work_fwd: int, work_fb: int, unit: str, sample: str,
+             budget: float) -> dict:
+    """The reference's eager torch path on the host CPU (the oracle's restatement of its
+    reference() formulas + autograd): forward and forward+backward, in bf16 (as the eager model
+    runs) and fp32. Rates are the sample's algorithmic work over its median time; the work is
+    linear in the sampled rows or (batch, head) pairs, so the full workload's CPU time is its
+    work over the same rate. The headline leg is forward+backward in bf16."""
+    import krsi_oracle as O
+    scale = 1e9 if unit == "GB/s" else 1e12
+    legs = {}
+    for dname, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        cast = {k: (v.to(dt) if isinstance(v, torch.Tensor) and v.is_floating_point() and k != "pd" else v)
+                for k, v in inputs.items()}
+        for mode, work in (("fwd", work_fwd), ("fwd_bwd", work_fb)):
+            args = {**cast, "fwd_only": mode == "fwd"}
+            sec, reps = _cpu_seconds(lambda: O.cpu_eager_step(kind, args), budget)
+            legs[f"{mode}_{dname}"] = {"value": round(work / sec / scale, 4), "unit": unit,
+                                       "median_s": round(sec, 5), "reps": reps}
+    head = legs["fwd_bwd_bf16"]
+    return {"value": head["value"], "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{sample}; fwd+bwd bf16, median of {head['reps']} reps",
+            "extrapolation": "rate = the sample's algorithmic work / its median time; work is linear "
+                             "in the sampled rows or (batch, head) pairs",
+            "legs": legs}
+
+
 # ------------------------------------------------------------------- workloads
 def bench_rmsnorm(args) -> dict:
     import _hip
     rows, n, eps = 32768, 4096, 1e-6
-    x = _gen((rows, n), 0).cuda()
+    nset, lag = 4, 2  # 4 x (x + g) = 2.1 GB of inputs
+    xs = [_gen((rows, n), 0 if i == 0 else 100 + i) for i in range(nset)]
+    gs = [_gen((rows, n), 2 if i == 0 else 200 + i) for i in range(nset)]
+    x_dev = [x.cuda() for x in xs]
+    g_dev = [g.cuda() for g in gs]
     w = _gen((n,), 1, std=0.02, mean=1.0).cuda()
-    g = _gen((rows, n), 2).cuda()
     st = torch.cuda.current_stream()
-    state = {}
+    rstd = [_hip.rmsnorm_fwd(x, w, eps)[1] for x in x_dev]
 
-    def step():
-        y, rstd = _hip.rmsnorm_fwd(x, w, eps)
-        state["r"] = _hip.rmsnorm_bwd(g, x, w, rstd)
+    def fwd(i):
+        rstd[i] = _hip.rmsnorm_fwd(x_dev[i], w, eps)[1]
 
-    t = _time_steps(step, args.steps, args.warmup, st)
-    # Per-kernel: forward and backward timed separately with the same protocol.
-    _, rstd = _hip.rmsnorm_fwd(x, w, eps)
-    tf = _time_steps(lambda: _hip.rmsnorm_fwd(x, w, eps), args.steps, args.warmup, st)
-    tb = _time_steps(lambda: _hip.rmsnorm_bwd(g, x, w, rstd), args.steps, args.warmup, st)
+    def bwd(i):
+        _hip.rmsnorm_bwd(g_dev[i], x_dev[i], w, rstd[i])
+
+    t = _time_steps(_pipelined(fwd, bwd, nset, lag), args.steps, args.warmup, st)
+    tf = _time_steps(_rotating(fwd, nset), args.steps, args.warmup, st)
+    tb = _time_steps(_rotating(bwd, nset), args.steps, args.warmup, st)
+    warm = _time_steps(lambda: (fwd(0), bwd(0)), args.steps, args.warmup, st)
     fwd_b = 4 * rows * n + 4 * rows + 2 * n          # x in, y out, rstd out, w in
     bwd_b = 6 * rows * n + 4 * rows + 4 * n          # g, x in, dx out, rstd in, w in, dw out
     total = fwd_b + bwd_b
-    gbs = total / (t["ms_mean"] * 1e-3) / 1e9
+    gbs = _rate(total, t["ms_mean"], 1e9)
     res = {"workload": "rmsnorm fwd+bwd x[8,4096,4096] bf16 (BASELINE config 2)", "value": round(gbs, 1),
-           "unit": "GB/s", "ms_per_step": round(t["ms_mean"], 4), "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_bytes": total,
-           "kernels": {"rmsnorm_fwd": {"ms": round(tf["ms_mean"], 4), "bytes": fwd_b,
-                                       "GB/s": round(fwd_b / tf["ms_mean"] / 1e6, 1)},
-                       "rmsnorm_bwd": {"ms": round(tb["ms_mean"], 4), "bytes": bwd_b,
-                                       "GB/s": round(bwd_b / tb["ms_mean"] / 1e6, 1)}},
-           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
+           "unit": "GB/s", "ms_per_step": round(t["ms_mean"], 4), "host_enqueue_ms_per_step": round(t["host_ms"], 4),
+           "algorithmic_bytes": total,
+           "rotation": f"{nset} input sets (x, g: {nset * 4 * rows * n / 1e9:.2f} GB), backward lags forward by {lag}",
+           "kernels": {"rmsnorm_fwd": _kernel_line(tf["ms_mean"], fwd_b, "GB/s"),
+                       "rmsnorm_bwd": _kernel_line(tb["ms_mean"], bwd_b, "GB/s")},
+           "mall_warm": {"ms_per_step": round(warm["ms_mean"], 4),
+                         "GB/s": round(_rate(total, warm["ms_mean"], 1e9), 1),
+                         "note": "forward and backward of one set back to back: x partly MALL-resident"},
+           "roofline": _roofline(gbs, "GB/s")}
     if not args.no_cpu:
-        import krsi_oracle as O
         sr = 1024  # bounded sample: 1024 of the 32768 rows
-        xs, gs, ws = x[:sr].cpu(), g[:sr].cpu(), w.cpu()
-        sec, reps = _cpu_time(lambda: O.cpu_eager_step("rmsnorm", {"x": xs, "w": ws, "g": gs, "eps": eps}))
-        sb = 10 * sr * n + 8 * sr + 6 * n
-        res["cpu_baseline"] = {"value": round(sb / sec / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
-                               "kind": "port", "sample": f"reference eager torch fwd+bwd (bf16) on {sr} of {rows} rows, "
-                                                         f"median of {reps} reps"}
+        res["cpu_baseline"] = cpu_legs(
+            "rmsnorm", {"x": xs[0][:sr], "w": w.cpu(), "g": gs[0][:sr], "eps": eps},
+            4 * sr * n + 4 * sr + 2 * n, 10 * sr * n + 8 * sr + 6 * n, "GB/s",
+            f"{sr} of {rows} rows", args.cpu_seconds)
     return res
 
 
 def bench_geglu(args, approximate="none") -> dict:
     import _hip
     rows, f = 8192, 4096
-    ncopy = 2  # rotate two input sets (working set 2 x 402 MB > 256 MB MALL)
-    us = [_gen((rows, 2 * f), 10 * i).cuda() for i in range(ncopy)]
-    gs = [_gen((rows, f), 10 * i + 2).cuda() for i in range(ncopy)]
+    nset, lag = 6, 3  # 6 x (u + g) = 1.2 GB of inputs
+    us = [_gen((rows, 2 * f), 0 if i == 0 else 100 + i) for i in range(nset)]
+    gs = [_gen((rows, f), 2 if i == 0 else 200 + i) for i in range(nset)]
+    u_dev = [u.cuda() for u in us]
+    g_dev = [g.cuda() for g in gs]
     st = torch.cuda.current_stream()
-    it = [0]
 
-    def step():
-        i = it[0] % ncopy
-        it[0] += 1
-        _hip.geglu_fwd(us[i], approximate)
-        _hip.geglu_bwd(gs[i], us[i], approximate)
+    def fwd(i):
+        _hip.geglu_fwd(u_dev[i], approximate)
 
-    t = _time_steps(step, args.steps, args.warmup, st)
-    tf = _time_steps(lambda: _hip.geglu_fwd(us[it[0] % ncopy], approximate), args.steps, args.warmup, st)
-    tb = _time_steps(lambda: _hip.geglu_bwd(gs[0], us[0], approximate), args.steps, args.warmup, st)
+    def bwd(i):
+        _hip.geglu_bwd(g_dev[i], u_dev[i], approximate)
+
+    t = _time_steps(_pipelined(fwd, bwd, nset, lag), args.steps, args.warmup, st)
+    tf = _time_steps(_rotating(fwd, nset), args.steps, args.warmup, st)
+    tb = _time_steps(_rotating(bwd, nset), args.steps, args.warmup, st)
+    warm = _time_steps(lambda: (fwd(0), bwd(0)), args.steps, args.warmup, st)
     fwd_b, bwd_b = 6 * rows * f, 10 * rows * f
     total = fwd_b + bwd_b
-    gbs = total / (t["ms_mean"] * 1e-3) / 1e9
-    res = {"workload": f"geglu fwd+bwd u[4,2048,8192] bf16, gelu {'erf' if approximate == 'none' else 'tanh'} "
-                       "(BASELINE config 3)", "value": round(gbs, 1), "unit": "GB/s",
-           "ms_per_step": round(t["ms_mean"], 4), "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_bytes": total,
-           "kernels": {"geglu_fwd": {"ms": round(tf["ms_mean"], 4), "bytes": fwd_b,
-                                     "GB/s": round(fwd_b / tf["ms_mean"] / 1e6, 1)},
-                       "geglu_bwd": {"ms": round(tb["ms_mean"], 4), "bytes": bwd_b,
-                                     "GB/s": round(bwd_b / tb["ms_mean"] / 1e6, 1)}},
-           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}}
+    gbs = _rate(total, t["ms_mean"], 1e9)
+    form = "erf" if approximate == "none" else "tanh"
+    res = {"workload": f"geglu fwd+bwd u[4,2048,8192] bf16, gelu {form} (BASELINE config 3)",
+           "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(t["ms_mean"], 4),
+           "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_bytes": total,
+           "rotation": f"{nset} input sets (u, g: {nset * 6 * rows * f / 1e9:.2f} GB), backward lags forward by {lag}",
+           "kernels": {"geglu_fwd": _kernel_line(tf["ms_mean"], fwd_b, "GB/s"),
+                       "geglu_bwd": _kernel_line(tb["ms_mean"], bwd_b, "GB/s")},
+           "mall_warm": {"ms_per_step": round(warm["ms_mean"], 4),
+                         "GB/s": round(_rate(total, warm["ms_mean"], 1e9), 1),
+                         "note": "forward and backward of one set back to back: u partly MALL-resident"},
+           "roofline": _roofline(gbs, "GB/s")}
     if not args.no_cpu:
-        import krsi_oracle as O
         sr = 512
-        u_s, g_s = us[0][:sr].cpu(), gs[0][:sr].cpu()
-        sec, reps = _cpu_time(lambda: O.cpu_eager_step("geglu", {"u": u_s, "g": g_s, "approximate": approximate}))
-        res["cpu_baseline"] = {"value": round(16 * sr * f / sec / 1e9, 2), "unit": "GB/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"reference eager torch fwd+bwd (bf16) on {sr} of {rows} rows, "
-                                         f"median of {reps} reps"}
+        res["cpu_baseline"] = cpu_legs(
+            "geglu", {"u": us[0][:sr], "g": gs[0][:sr], "approximate": approximate},
+            6 * sr * f, 16 * sr * f, "GB/s", f"{sr} of {rows} rows", args.cpu_seconds)
     return res
 
 
-def bench_relpos(args, B=4, S=4096, H=16, D=64, fwd_only=False, dtype=torch.bfloat16) -> dict:
+def bench_relpos(args, B=4, S=4096, H=16, D=64, dtype=torch.bfloat16) -> dict:
     import _hip
     scale = 1.0 / math.sqrt(D)
-    qkv = _gen((B * S, 3 * H * D), 0, dtype=dtype).cuda()
-    pd = _gen((H, 2 * S - 1), 1, std=0.02, dtype=torch.float32).cuda()
-    dout = _gen((B * S, H * D), 2, dtype=dtype).cuda()
+    nset, lag = 4, 2  # 4 x (qkv + dout) = 0.54 GB of inputs, plus per-set out32 and lse
     dname = "bf16" if dtype == torch.bfloat16 else "fp16"
+    qkvs = [_gen((B * S, 3 * H * D), 0 if i == 0 else 100 + i, dtype=dtype) for i in range(nset)]
+    douts = [_gen((B * S, H * D), 2 if i == 0 else 200 + i, dtype=dtype) for i in range(nset)]
+    qkv_dev = [q.cuda() for q in qkvs]
+    dout_dev = [d.cuda() for d in douts]
+    pd = _gen((H, 2 * S - 1), 1, std=0.02, dtype=torch.float32).cuda()
     st = torch.cuda.current_stream()
+    saved = [_hip.relpos_fwd(q, pd, B, S, H, D, scale)[1:] for q in qkv_dev]
+
+    def fwd(i):
+        saved[i] = _hip.relpos_fwd(qkv_dev[i], pd, B, S, H, D, scale)[1:]
+
+    def bwd(i):
+        _hip.relpos_bwd(dout_dev[i], qkv_dev[i], pd, *saved[i], B, S, H, D, scale)
+
     fl_fwd = 4 * B * H * S * S * D
     fl_bwd = 10 * B * H * S * S * D
-    _, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, scale)
-    tf = _time_steps(lambda: _hip.relpos_fwd(qkv, pd, B, S, H, D, scale), args.steps, args.warmup, st)
-    if fwd_only:
-        tfl = fl_fwd / (tf["ms_mean"] * 1e-3) / 1e12
-        return {"workload": f"relpos attention fwd B{B} H{H} L{S} D{D} bf16 (BASELINE config 4)",
-                "value": round(tfl, 1), "unit": "TFLOP/s", "ms_per_step": round(tf["ms_mean"], 4), "host_enqueue_ms_per_step": round(tf["host_ms"], 4),
-                "algorithmic_flops": fl_fwd,
-                "roofline": {"bound": "mfma", "achieved": round(tfl, 1), "peak": PEAK_BF16_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(tfl / PEAK_BF16_TFLOPS, 4), "traffic": None}}
-
-    def step():
-        o, o32, l = _hip.relpos_fwd(qkv, pd, B, S, H, D, scale)
-        _hip.relpos_bwd(dout, qkv, pd, o32, l, B, S, H, D, scale)
-
-    t = _time_steps(step, args.steps, args.warmup, st)
-    tb = _time_steps(lambda: _hip.relpos_bwd(dout, qkv, pd, out32, lse, B, S, H, D, scale),
-                     args.steps, args.warmup, st)
     total = fl_fwd + fl_bwd
-    tfl = total / (t["ms_mean"] * 1e-3) / 1e12
+    t = _time_steps(_pipelined(fwd, bwd, nset, lag), args.steps, args.warmup, st)
+    tf = _time_steps(_rotating(fwd, nset), args.steps, args.warmup, st)
+    tb = _time_steps(_rotating(bwd, nset), args.steps, args.warmup, st)
+    warm = _time_steps(lambda: (fwd(0), bwd(0)), args.steps, args.warmup, st)
+    tfl = _rate(total, t["ms_mean"], 1e12)
+    suffix = ")" if dname == "bf16" else " shape, fp16 activations)"
     res = {"workload": f"relpos attention fwd+bwd B{B} H{H} L{S} D{D} {dname}, pd fp32 [H,2L-1] "
-                       "(BASELINE config 5" + (")" if dname == "bf16" else " shape, fp16 activations)"),
-           "value": round(tfl, 2), "unit": "TFLOP/s",
-           "ms_per_step": round(t["ms_mean"], 4), "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_flops": total,
-           "kernels": {"relpos_fwd": {"ms": round(tf["ms_mean"], 4), "flops": fl_fwd,
-                                      "TFLOP/s": round(fl_fwd / tf["ms_mean"] / 1e9, 1)},
-                       "relpos_bwd (dq+delta+dpd, dkdv, dpd reduce)": {
-                           "ms": round(tb["ms_mean"], 4), "flops": fl_bwd,
-                           "TFLOP/s": round(fl_bwd / tb["ms_mean"] / 1e9, 1)}},
-           "roofline": {"bound": "mfma", "achieved": round(tfl, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tfl / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                       f"(BASELINE config 5{suffix}",
+           "value": round(tfl, 2), "unit": "TFLOP/s", "ms_per_step": round(t["ms_mean"], 4),
+           "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_flops": total,
+           "rotation": f"{nset} input sets (qkv, dout), backward lags forward by {lag}",
+           "kernels": {"relpos_fwd": _kernel_line(tf["ms_mean"], fl_fwd, "TFLOP/s"),
+                       "relpos_bwd (dq+delta+dpd, dkdv, dpd reduce)": _kernel_line(tb["ms_mean"], fl_bwd, "TFLOP/s")},
+           "mall_warm": {"ms_per_step": round(warm["ms_mean"], 4),
+                         "TFLOP/s": round(_rate(total, warm["ms_mean"], 1e12), 1)},
+           "roofline": {**_roofline(tfl, "TFLOP/s"),
                         "scope": "one fwd+bwd step = relpos_fwd_kernel + relpos_bwd_dq_kernel + "
                                  "relpos_bwd_dkdv_kernel + relpos_dpd_reduce4, 14*B*H*L^2*D flops"}}
     if not args.no_cpu and dname == "bf16":
-        import krsi_oracle as O
         nb = 2  # bounded sample: 2 of the B*H = 64 (batch, head) pairs, full L
-        qs = qkv.view(B, S, 3, H, D)[0, :, :, :nb].reshape(S, 3 * nb * D).cpu()
-        ps, ds_ = pd[:nb].cpu(), dout.view(B, S, H, D)[0, :, :nb].reshape(S, nb * D).cpu()
-        sec, reps = _cpu_time(lambda: O.cpu_eager_step("relpos", {"qkv": qs, "pd": ps, "dout": ds_,
-                                                                  "dims": (1, S, nb, D), "scale": scale}),
-                              min_s=10.0, max_reps=10)
-        res["cpu_baseline"] = {"value": round(14 * nb * S * S * D / sec / 1e12, 4), "unit": "TFLOP/s",
-                               "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"reference eager torch SDPA-MATH fwd+bwd (bf16 in, fp32 math) on "
-                                         f"{nb} of {B * H} (batch, head) pairs at L={S}, median of {reps} reps"}
+        q0, d0 = qkvs[0], douts[0]
+        sample = {"qkv": q0.view(B, S, 3, H, D)[0, :, :, :nb].reshape(S, 3 * nb * D).clone(),
+                  "pd": pd[:nb].cpu(), "dout": d0.view(B, S, H, D)[0, :, :nb].reshape(S, nb * D).clone(),
+                  "dims": (1, S, nb, D), "scale": scale}
+        res["cpu_baseline"] = cpu_legs("relpos", sample, 4 * nb * S * S * D, 14 * nb * S * S * D, "TFLOP/s",
+                                       f"SDPA-MATH on {nb} of {B * H} (batch, head) pairs at L={S}",
+                                       args.cpu_seconds)
     return res
 
 
+def bench_relpos_fwd_config4(args) -> dict:
+    import _hip
+    B, S, H, D = 2, 1024, 16, 72
+    scale = 1.0 / math.sqrt(D)
+    nset = 16  # 16 x 14.2 MB of qkv, 16 x 21 MB of outputs
+    qkv_dev = [_gen((B * S, 3 * H * D), 0 if i == 0 else 100 + i).cuda() for i in range(nset)]
+    pd = _gen((H, 2 * S - 1), 1, std=0.02, dtype=torch.float32).cuda()
+    st = torch.cuda.current_stream()
+    t = _time_steps(_rotating(lambda i: _hip.relpos_fwd(qkv_dev[i], pd, B, S, H, D, scale), nset),
+                    args.steps, args.warmup, st)
+    fl = 4 * B * H * S * S * D
+    tfl = _rate(fl, t["ms_mean"], 1e12)
+    return {"workload": f"relpos attention fwd B{B} H{H} L{S} D{D} bf16 (BASELINE config 4)",
+            "value": round(tfl, 1), "unit": "TFLOP/s", "ms_per_step": round(t["ms_mean"], 4),
+            "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_flops": fl,
+            "rotation": f"{nset} input sets", "roofline": _roofline(tfl, "TFLOP/s")}
+
+
+def bench_selftest_shapes(args) -> dict:
+    """The reference's selftest() shapes (its only published timings, on an H20-3e), timed as
+    that selftest times them: one input set, forward + backward back to back. These working
+    sets (8-40 MB) fit the MALL, so the rates are cache-assisted by construction."""
+    import _hip
+    st = torch.cuda.current_stream()
+    out = {}
+    rows, n = 4096, 1024
+    x, g = _gen((rows, n), 0).cuda(), _gen((rows, n), 2).cuda()
+    w = _gen((n,), 1, std=0.1, mean=1.0).cuda()
+    t = _time_steps(lambda: _hip.rmsnorm_bwd(g, x, w, _hip.rmsnorm_fwd(x, w, 1e-6)[1]), args.steps, args.warmup, st)
+    work = 10 * rows * n + 8 * rows + 6 * n
+    out["rmsnorm"] = (f"rmsnorm fwd+bwd x[{rows},{n}] bf16", t, work, "GB/s")
+    rows, f = 2048, 2816
+    u, gg = _gen((rows, 2 * f), 0).cuda(), _gen((rows, f), 2).cuda()
+    t = _time_steps(lambda: (_hip.geglu_fwd(u, "tanh"), _hip.geglu_bwd(gg, u, "tanh")), args.steps, args.warmup, st)
+    out["geglu"] = (f"geglu fwd+bwd u[{rows},{2 * f}] bf16, gelu tanh", t, 16 * rows * f, "GB/s")
+    B, S, H, D = 4, 512, 16, 64
+    qkv = (0.6 * _gen((B * S, 3 * H * D), 0, dtype=torch.float32)).to(torch.bfloat16).cuda()
+    pd = _gen((H, 2 * S - 1), 1, dtype=torch.float32).cuda()
+    dout = _gen((B * S, H * D), 2).cuda()
+
+    def attn():
+        _, o32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, 1.0)
+        _hip.relpos_bwd(dout, qkv, pd, o32, lse, B, S, H, D, 1.0)
+    t = _time_steps(attn, args.steps, args.warmup, st)
+    out["relpos_attention"] = (f"relpos attention fwd+bwd B{B} S{S} H{H} D{D} bf16, scale 1", t,
+                               14 * B * H * S * S * D, "TFLOP/s")
+    res = {}
+    for name, (wl, t, work, unit) in out.items():
+        v = _rate(work, t["ms_mean"], 1e9 if unit == "GB/s" else 1e12)
+        us = t["ms_mean"] * 1e3
+        res[name] = {"workload": wl, "us_per_step": round(us, 1), "value": round(v, 1), "unit": unit,
+                     "roofline": _roofline(v, unit), "h20_reference_kernel_us": H20_SELFTEST_US[name],
+                     "vs_h20_reference_kernel": round(H20_SELFTEST_US[name] / us, 2),
+                     "host_enqueue_us_per_step": round(t["host_ms"] * 1e3, 1)}
+    return res
+
+
+def bench_config1(args) -> dict:
+    """the RMSNorm forward the reference runs on its CPU path, x [2,1024,1152]
+    and the ragged [1,300,1152]. The CPU figure (full size, no sampling) is the headline here;
+    the GPU forward is timed beside it (launch-latency bound at this size)."""
+    import _hip
+    n, eps = 1152, 1e-6
+    st = torch.cuda.current_stream()
+    w = _gen((n,), 1, std=0.02, mean=1.0)
+    res = {}
+    for name, rows in (("x[2,1024,1152]", 2048), ("x[1,300,1152]", 300)):
+        x = _gen((rows, n), 0)
+        work = 4 * rows * n + 4 * rows + 2 * n
+        xd, wd = x.cuda(), w.cuda()
+        t = _time_steps(lambda: _hip.rmsnorm_fwd(xd, wd, eps), args.steps, args.warmup, st)
+        entry = {"gpu_fwd_us": round(t["ms_mean"] * 1e3, 2),
+                 "gpu_fwd_GB/s": round(_rate(work, t["ms_mean"], 1e9), 1), "algorithmic_bytes": work}
+        if not args.no_cpu:
+            import krsi_oracle as O
+            for dname, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+                inp = {"x": x.to(dt), "w": w.to(dt), "eps": eps, "fwd_only": True}
+                sec, reps = _cpu_seconds(lambda: O.cpu_eager_step("rmsnorm", inp), min(args.cpu_seconds, 2.0), 200)
+                entry[f"cpu_fwd_{dname}"] = {"us": round(sec * 1e6, 1), "GB/s": round(work / sec / 1e9, 2),
+                                             "reps": reps, "cores": torch.get_num_threads()}
+        res[name] = entry
+    return {"workload": "rmsnorm fwd on the reference's CPU path, eps 1e-6 (BASELINE config 1)", "shapes": res}
+
+
+# ------------------------------------------------------------------- traffic
 def _csrc_sha256() -> str:
     import hashlib
     h = hashlib.sha256()
@@ -268,7 +452,7 @@ def attach_traffic(comps: dict) -> None:
     fresh = rec.get("csrc_sha256") == _csrc_sha256()
     for name, comp in comps.items():
         t = rec.get("components", {}).get(name)
-        if t is None:
+        if t is None or "roofline" not in comp:
             continue
         comp["roofline"]["traffic"] = t["bytes_per_step"] if fresh else None
         comp["roofline"]["traffic_unit"] = "bytes per step (HBM read + write)"
@@ -296,13 +480,17 @@ def measured_copy_gbs() -> float:
     return round(2 * 2 * n / (ms * 1e-3) / 1e9, 1)
 
 
+ALL = "relpos,relpos_fwd,relpos_fp16,rmsnorm,geglu,selftest_shapes,config1"
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="relpos,relpos_fwd,rmsnorm,geglu,relpos_fp16")
+    ap.add_argument("--only", default=ALL)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU time budget per CPU-baseline leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's kernels run on one MI355X and no "
@@ -317,23 +505,29 @@ def main() -> None:
     if "relpos" in only:
         comps["relpos_attention"] = bench_relpos(args)
     if "relpos_fwd" in only:
-        comps["relpos_attention_fwd_config4"] = bench_relpos(args, B=2, S=1024, H=16, D=72, fwd_only=True)
+        comps["relpos_attention_fwd_config4"] = bench_relpos_fwd_config4(args)
     if "relpos_fp16" in only:
         comps["relpos_attention_fp16"] = bench_relpos(args, dtype=torch.float16)
     if "rmsnorm" in only:
         comps["rmsnorm"] = bench_rmsnorm(args)
     if "geglu" in only:
         comps["geglu"] = bench_geglu(args, "none")
+    if "selftest_shapes" in only:
+        comps["selftest_shapes"] = bench_selftest_shapes(args)
+    if "config1" in only:
+        comps["rmsnorm_config1"] = bench_config1(args)
     attach_traffic(comps)
-    head = comps.get("relpos_attention") or next(iter(comps.values()))
+    head = comps.get("relpos_attention") or next(c for c in comps.values() if "value" in c)
+    cpu = cpu_model()
     line = {
         "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded CPU randn, BASELINE shapes)",
         "config": {"workload": head["workload"], "device": torch.cuda.get_device_name(0)},
         "roofline": head["roofline"],
-        "cpu_baseline": {**head.get("cpu_baseline", {}), "cpu": _cpu_model()} if "cpu_baseline" in head else None,
+        "cpu_baseline": {**head["cpu_baseline"], "cpu": cpu["model"]} if "cpu_baseline" in head else None,
         "components": comps,
+        "host_cpu": cpu,
         "measured_peaks": {"hbm_copy_GB/s": measured_copy_gbs()},
     }
     print(json.dumps(line))

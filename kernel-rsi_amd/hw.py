@@ -1,124 +1,191 @@
 #!/usr/bin/env python3
-"""Measure this GPU's achievable peaks and write them to hardware/<device slug>.json.
+"""Measured ceilings of this GPU, written to hardware/<gpu>.json.
 
-  python kernel-rsi_amd/hw.py
+  python kernel-rsi_amd/hw.py [--quick]
 
-Mirrors the reference's tools/hw.py (:90-178) for an MI355X: dense GEMM TFLOP/s per dtype as
-the vendor library (hipBLASLt through torch.matmul) reaches them, skinny-GEMM rates, copy / read
-/ write GB/s, launch costs (one torch op, one graph replay), and the derived ridge points. The
-roofline fractions elsewhere in this package use the published peaks (HBM 8.0 TB/s, bf16 dense
-2.5 PFLOP/s); these measured ceilings are reported beside them. NVIDIA-only probes of the
-reference (Triton launch probe, ncu availability) have no counterpart here.
+The reference's tools read two things from such a record: `tflops[dtype]` and
+`bw_copy_gbs` / `bw_read_gbs` (tools/common.py:56-64; its own probe is tools/hw.py). They use
+them as roofline denominators. This module fills those keys for an MI355X and adds what this
+package's roofline discussion uses:
+  * the published peaks;
+  * launch costs;
+  * the ridge points.
+The probes are a table of small functions. Each runs under `Clock`, which reports the median
+of per-call HIP event times after a warm-up. The bandwidth probes use 1 GiB buffers, far
+beyond the 4 MB L2 of each XCD and the 256 MB MALL, so every call streams HBM.
+
+The record is named after the product (AMD Instinct MI355X for gfx950 with 256 CUs), because
+torch reports a generic name on boxes without the marketing-name table. A copy is also kept
+under the slug of torch's device name, which is the file the reference's tools open on this
+machine.
 """
 from __future__ import annotations
 
+import argparse
 import json
+import statistics
 import sys
 from pathlib import Path
 
 import torch
 
 HERE = Path(__file__).resolve().parent
+PUBLISHED = {"hbm_gbs": 8000, "bf16_dense_tflops": 2500, "fp16_dense_tflops": 2500,
+             "fp8_dense_tflops": 5000, "fp32_tflops": 157.3}
 
 
 def slug(text: str) -> str:
     return "".join(c if c.isalnum() else "_" for c in text).strip("_").lower()
 
 
-def best_ms(fn, iters: int = 10, reps: int = 5) -> float:
-    """Best over reps of the mean event time of iters back-to-back calls, after a warm-up."""
-    fn()
-    torch.cuda.synchronize()
-    best = float("inf")
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(iters):
+def product_name(props) -> str:
+    """The marketing name of the part (torch says 'AMD Radeon Graphics' when the driver's name
+    table is absent, as on these boxes)."""
+    arch = props.gcnArchName.split(":")[0]
+    if arch == "gfx950" and props.multi_processor_count == 256:
+        return "AMD Instinct MI355X"
+    return props.name
+
+
+class Clock:
+    """Median device milliseconds of one call of fn (HIP events around `inner` calls)."""
+
+    def __init__(self, samples: int = 7):
+        self.samples = samples
+
+    def ms(self, fn, inner: int = 10) -> float:
+        for _ in range(3):
             fn()
-        e1.record()
         torch.cuda.synchronize()
-        best = min(best, e0.elapsed_time(e1) / iters)
-    return best
+        times = []
+        for _ in range(self.samples):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(inner):
+                fn()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b) / inner)
+        return statistics.median(times)
 
 
-def main() -> int:
-    if not torch.cuda.is_available():
-        raise SystemExit("no GPU")
-    props = torch.cuda.get_device_properties(0)
-    n = 8192
+def _square(n, dtype):
+    return torch.randn(n, n, device="cuda").to(dtype)
 
-    def gemm_tflops(dtype, iters=10):
-        a = torch.randn(n, n, device="cuda", dtype=dtype)
-        b = torch.randn(n, n, device="cuda", dtype=dtype)
-        t = 2 * n ** 3 / best_ms(lambda: a @ b, iters=iters) / 1e9
+
+def probe_gemm(clock: Clock, n: int) -> dict:
+    """Dense n^3 GEMM rate of the vendor library (hipBLASLt via torch.matmul) per dtype."""
+    out = {}
+    for key, dtype, inner in (("bf16", torch.bfloat16, 10), ("fp16", torch.float16, 10),
+                              ("fp32", torch.float32, 3)):
+        a, b = _square(n, dtype), _square(n, dtype)
+        prev = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False  # fp32 means fp32 here (gfx950 has no TF32)
+        try:
+            out[key] = round(2 * n ** 3 / clock.ms(lambda: torch.mm(a, b), inner) / 1e9, 1)
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = prev
         del a, b
-        return round(t, 1)
-
-    tflops = {"fp16": gemm_tflops(torch.float16), "bf16": gemm_tflops(torch.bfloat16)}
-    old_tf32 = torch.backends.cuda.matmul.allow_tf32
     try:
-        torch.backends.cuda.matmul.allow_tf32 = False
-        tflops["fp32"] = gemm_tflops(torch.float32, iters=3)
-    finally:
-        torch.backends.cuda.matmul.allow_tf32 = old_tf32
-    try:
-        a = torch.randn(n, n, device="cuda").to(torch.float8_e4m3fn)
-        b = torch.randn(n, n, device="cuda").to(torch.float8_e4m3fn).t().contiguous().t()
+        a = _square(n, torch.float8_e4m3fn)
+        bt = _square(n, torch.float8_e4m3fn).t()  # column-major right operand
         one = torch.ones((), device="cuda")
-        tflops["fp8"] = round(2 * n ** 3 / best_ms(
-            lambda: torch._scaled_mm(a, b, one, one, out_dtype=torch.bfloat16)) / 1e9, 1)
-        del a, b
-    except Exception as e:  # noqa: BLE001 - the fp8 GEMM entry point differs across builds
-        tflops["fp8_error"] = f"{type(e).__name__}: {str(e).splitlines()[0][:160]}"
-    skinny = {}
-    for m_ in (16, 64, 256, 1024):
-        a = torch.randn(m_, 4096, device="cuda", dtype=torch.bfloat16)
-        b = torch.randn(4096, 4096, device="cuda", dtype=torch.bfloat16)
-        skinny[f"M{m_}xN4096xK4096"] = round(2 * m_ * 4096 * 4096 / best_ms(lambda: a @ b, iters=50) / 1e9, 1)
-    tflops["skinny_bf16"] = skinny
-    torch.cuda.empty_cache()
+        out["fp8"] = round(2 * n ** 3 / clock.ms(
+            lambda: torch._scaled_mm(a, bt, one, one, out_dtype=torch.bfloat16)) / 1e9, 1)
+    except Exception as e:  # noqa: BLE001 - the fp8 GEMM entry point differs across torch builds
+        out["fp8_error"] = f"{type(e).__name__}: {str(e).splitlines()[0][:160]}"
+    return out
 
-    numel = 512 << 20  # 1 GiB per fp16 buffer: far beyond L2 and the 256 MB MALL
-    src = torch.randn(numel, device="cuda", dtype=torch.float16)
+
+def probe_skinny(clock: Clock) -> dict:
+    """bf16 GEMM rate with few rows (decode-like shapes), K = N = 4096."""
+    w = _square(4096, torch.bfloat16)
+    rates = {}
+    for m in (16, 64, 256, 1024):
+        x = torch.randn(m, 4096, device="cuda").to(torch.bfloat16)
+        rates[f"M{m}xN4096xK4096"] = round(2 * m * 4096 * 4096 / clock.ms(lambda: x @ w, 50) / 1e9, 1)
+    return rates
+
+
+def probe_bandwidth(clock: Clock) -> dict:
+    """GB/s of a device copy (read + write), a reduction (read) and a fill (write) of 1 GiB."""
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 2, device="cuda", dtype=torch.float16).normal_()
     dst = torch.empty_like(src)
-    copy = 4 * numel / best_ms(lambda: dst.copy_(src)) / 1e6
-    read = 2 * numel / best_ms(lambda: src.sum(dtype=torch.float32)) / 1e6
-    write = 2 * numel / best_ms(lambda: dst.fill_(1.0)) / 1e6
+    res = {
+        "bw_copy_gbs": 2 * nbytes / clock.ms(lambda: dst.copy_(src)) / 1e6,
+        "bw_read_gbs": nbytes / clock.ms(lambda: torch.sum(src, dtype=torch.float32)) / 1e6,
+        "bw_write_gbs": nbytes / clock.ms(lambda: dst.fill_(0.5)) / 1e6,
+    }
     del src, dst
     torch.cuda.empty_cache()
+    return {k: round(v) for k, v in res.items()}
 
+
+def probe_launch(clock: Clock) -> dict:
+    """Microseconds per tiny kernel: one stream launch of a torch op, one graph replay."""
     x = torch.zeros(1, device="cuda")
-    launch_torch = best_ms(lambda: x.add_(1.0), iters=200) * 1000
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
+    per_launch = clock.ms(lambda: x.add_(1.0), 200) * 1e3
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
         x.add_(1.0)
-    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         x.add_(1.0)
-    launch_graph = best_ms(g.replay, iters=200) * 1000
+    per_replay = clock.ms(g.replay, 200) * 1e3
+    return {"launch_us_torch": round(per_launch, 1), "launch_us_graph_replay": round(per_replay, 1)}
 
-    bw = max(copy, read)
-    info = {
-        "device": props.name, "arch": props.gcnArchName, "cus": props.multi_processor_count,
-        "l2_mb": round(getattr(props, "L2_cache_size", 0) / 2 ** 20, 1),
-        "memory_gb": round(props.total_memory / 2 ** 30, 1), "tflops": tflops,
-        "bw_copy_gbs": round(copy), "bw_read_gbs": round(read), "bw_write_gbs": round(write),
-        "ridge_flop_per_byte": {k: round(v * 1e12 / (bw * 1e9), 1) for k, v in tflops.items()
-                                if isinstance(v, (int, float))},
-        "published_peaks": {"hbm_gbs": 8000, "bf16_dense_tflops": 2500, "fp8_dense_tflops": 5000,
-                            "fp32_tflops": 157.3},
-        "default_half_dtype": "bf16", "features": {"bf16_mfma": True, "fp8": True},
-        "launch_us_torch": round(launch_torch, 1), "launch_us_graph_replay": round(launch_graph, 1),
-        "torch": torch.__version__, "hip": torch.version.hip,
-    }
-    path = HERE / "hardware" / f"{slug(props.name)}.json"
-    path.parent.mkdir(parents=True, exist_ok=True)
-    path.write_text(json.dumps(info, indent=2) + "\n")
-    for k, v in info.items():
-        print(f"{k:>24}: {v}")
-    print(f"saved {path}")
+
+def collect(quick: bool = False) -> dict:
+    props = torch.cuda.get_device_properties(0)
+    clock = Clock(samples=3 if quick else 7)
+    tflops = probe_gemm(clock, 4096 if quick else 8192)
+    tflops["skinny_bf16"] = probe_skinny(clock)
+    torch.cuda.empty_cache()
+    rec = {"device": product_name(props), "torch_device_name": props.name,
+           "arch": props.gcnArchName, "cus": props.multi_processor_count,
+           "l2_mb": round(getattr(props, "L2_cache_size", 0) / 2 ** 20, 1),
+           "memory_gb": round(props.total_memory / 2 ** 30, 1), "tflops": tflops}
+    rec.update(probe_bandwidth(clock))
+    stream_bw = max(rec["bw_copy_gbs"], rec["bw_read_gbs"])
+    rec["ridge_flop_per_byte"] = {k: round(v * 1e3 / stream_bw, 1) for k, v in tflops.items()
+                                  if isinstance(v, (int, float))}
+    rec["published_peaks"] = dict(PUBLISHED)
+    rec["default_half_dtype"] = "bf16"
+    rec["features"] = {"bf16_mfma": True, "fp8": True, "tf32": False}
+    rec.update(probe_launch(clock))
+    rec.update({"torch": torch.__version__, "hip": torch.version.hip})
+    return rec
+
+
+def write(rec: dict, root: Path = HERE / "hardware") -> list[Path]:
+    """The record under the product's name and, if it differs, under torch's device name."""
+    root.mkdir(parents=True, exist_ok=True)
+    paths = [root / f"{slug(rec['device'])}.json"]
+    alias = root / f"{slug(rec['torch_device_name'])}.json"
+    if alias != paths[0]:
+        paths.append(alias)
+    text = json.dumps(rec, indent=2) + "\n"
+    for p in paths:
+        p.write_text(text)
+    return paths
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--quick", action="store_true", help="smaller GEMM and fewer samples")
+    ap.add_argument("--out-dir", type=Path, default=HERE / "hardware", help="where the record goes")
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        raise SystemExit("hw.py measures a GPU; none is visible")
+    rec = collect(args.quick)
+    width = max(map(len, rec))
+    for k, v in rec.items():
+        print(f"{k:>{width}}  {v}")
+    for p in write(rec, args.out_dir):
+        print(f"wrote {p}")
     return 0
 
 

@@ -1,10 +1,11 @@
-"""GEGLU forward + backward on a merged [a | b] GEMM output, on hand-written gfx950 (MI355X)
-HIP kernels. Use geglu(u) (differentiable, torch.compile-friendly).
+"""Gated GELU of a fused gate|up projection, on gfx950 (MI355X) HIP kernels: geglu(u).
 
-u: [rows, 2F] (the output of x @ cat([W_gate, W_up]).T); returns gelu_tanh(u[:, :F]) * u[:, F:], with
-the same bf16 rounding points as eager. Backward writes d[a | b] in one pass, so the merged GEMM's
-backward reads one gradient tensor. geglu(u, approximate="none") selects the exact (erf) GELU.
-Drop-in for the reference's library/geglu.py (same functions and arguments; geglu.py:104-120).
+u is [rows, 2F]: the gate half a = u[:, :F] and the linear half b = u[:, F:], as one merged GEMM
+produces them. The result is gelu(a) * b, with gelu(a) rounded to u's dtype before the
+product, as in eager torch. The default is the tanh form. geglu(u, approximate="none") gives
+the erf form. The backward writes the gradient of both halves into one [rows, 2F] tensor in
+one pass, so the merged GEMM's backward takes a single gradient. Same public functions and
+arguments as the reference's library/geglu.py:104-120; usable under torch.compile(fullgraph=True).
 """
 import sys
 from pathlib import Path

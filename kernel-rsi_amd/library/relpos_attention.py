@@ -1,14 +1,15 @@
-"""Flash attention forward + backward with an additive bias that depends only on (j - i), on
-hand-written gfx950 (MI355X) HIP kernels (bf16 or fp16 MFMA, fp32 softmax).
+"""Non-causal flash attention with a learned bias indexed by key - query distance, forward and
+backward, on gfx950 (MI355X) HIP kernels: bf16 or fp16 MFMA with fp32 softmax.
 
-relpos_attention(qkv, pd, B, S, H, D, scale) -> [B*S, H*D]   (differentiable, torch.compile-friendly)
-  qkv: [B*S, 3*H*D] (the fused q|k|v GEMM output, read in place: no permute copies; any row stride)
-  pd:  [H, 2S-1] fp32 per-distance bias, bias[h, i, j] = pd[h, j - i + S - 1] (T5 relative position,
-       ALiBi, any Toeplitz bias); its gradient is reduced along the diagonals of dS inside the
-       backward kernels (no [B, H, S, S] buffer, no scatter).
-Backward keeps an fp32 copy of O for delta = rowsum(dO * O). No causal mask; D % 8 == 0, D <= 128
-(so D = 72 runs too). Drop-in for the reference's library/relpos_attention.py (same functions and
-arguments; relpos_attention.py:198-222).
+relpos_attention(qkv, pd, B, S, H, D, scale) returns [B*S, H*D].
+  qkv  [B*S, 3*H*D]: the fused projection output, read in place. Token t holds q, k and v of
+       head h at columns h*D, H*D + h*D and 2*H*D + h*D. Any row stride that is a multiple of 8.
+  pd   [H, 2S-1] fp32: the bias of query i and key j in head h is pd[h, j - i + S - 1]. This
+       covers T5 relative positions, ALiBi and any other Toeplitz bias.
+The backward keeps the fp32 output to form delta_i = sum_d dO_id * O_id. It sums dS along its
+diagonals inside the kernels to form pd's gradient. No [B, H, S, S] tensor is ever allocated.
+D may be any multiple of 8 up to 128 (D = 72 runs). Same public functions and arguments as the
+reference's library/relpos_attention.py:198-222; usable under torch.compile(fullgraph=True).
 """
 import math
 import sys

@@ -1,10 +1,13 @@
-"""RMSNorm forward + backward on hand-written gfx950 (MI355X) HIP kernels.
-Use rmsnorm(x2d, weight, eps) (differentiable, torch.compile-friendly).
+"""RMSNorm with its backward, on gfx950 (MI355X) HIP kernels: rmsnorm(x2d, weight, eps).
 
-y = weight * (x * rsqrt(mean(x^2) + eps)).to(x.dtype)   -- rounding as in HF T5LayerNorm / LlamaRMSNorm
-Forward saves an fp32 rstd per row; backward computes dx in one pass and dw as deterministic
-per-workgroup fp32 partial sums reduced in a fixed order (no atomics). Rows up to N = 16384.
-Drop-in for the reference's library/rmsnorm.py (same functions and arguments; rmsnorm.py:106-123).
+Each row is scaled by the reciprocal root of its mean square (fp32 arithmetic). The normalised
+row is rounded to the input dtype before it is multiplied by the weight, as the reference
+formula below (and the eager models it stands in for) does. The forward keeps one fp32
+reciprocal root per row for the backward. The backward writes dx in a single pass over the rows.
+The weight gradient is summed into per-workgroup fp32 partial rows, which two small launches
+then add in a fixed order, so dw is bitwise reproducible. Row lengths up to 16384.
+Same public functions and arguments as the reference's library/rmsnorm.py:106-123; usable under
+torch.compile(fullgraph=True).
 """
 import sys
 from pathlib import Path

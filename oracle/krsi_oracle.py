@@ -338,20 +338,24 @@ def randn(shape, seed: int, std: float = 1.0, mean: float = 0.0, dtype=torch.bfl
 
 # ------------------------------------------------- CPU baseline (eager path)
 def cpu_eager_step(kind: str, inputs: dict):
-    """One fwd+bwd of the reference's eager torch path on the CPU (the cpu_baseline leg)."""
+    """One fwd+bwd (or, with inputs["fwd_only"], one forward) of the reference's eager torch
+    path on the CPU, in the inputs' dtype (the cpu_baseline legs)."""
+    fwd_only = inputs.get("fwd_only", False)
+
+    def leaves(*names):
+        return [inputs[n].detach().requires_grad_(not fwd_only) for n in names]
+
     if kind == "rmsnorm":
-        x = inputs["x"].detach().requires_grad_(True)
-        w = inputs["w"].detach().requires_grad_(True)
+        x, w = leaves("x", "w")
         y = rmsnorm(x, w, inputs["eps"])
-        return torch.autograd.grad(y, [x, w], inputs["g"])
+        return y if fwd_only else torch.autograd.grad(y, [x, w], inputs["g"])
     if kind == "geglu":
-        u = inputs["u"].detach().requires_grad_(True)
+        (u,) = leaves("u")
         out = geglu(u, inputs.get("approximate", "tanh"))
-        return torch.autograd.grad(out, [u], inputs["g"])
+        return out if fwd_only else torch.autograd.grad(out, [u], inputs["g"])
     if kind == "relpos":
-        qkv = inputs["qkv"].detach().requires_grad_(True)
-        pd = inputs["pd"].detach().requires_grad_(True)
+        qkv, pd = leaves("qkv", "pd")
         B, S, H, D = inputs["dims"]
         out = relpos_sdpa(qkv, pd, B, S, H, D, inputs["scale"])
-        return torch.autograd.grad(out, [qkv, pd], inputs["dout"])
+        return out if fwd_only else torch.autograd.grad(out, [qkv, pd], inputs["dout"])
     raise ValueError(kind)
