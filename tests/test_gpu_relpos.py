@@ -120,6 +120,18 @@ def test_relpos_train_config5():
     assert (dpd.sum(1).abs() <= 1e-3 * dpd.abs().sum(1) + 1e-4).all()
 
 
+@pytest.mark.parametrize("S", [8191, 16384])
+def test_relpos_long_sequence(S):
+    """Long context, B1 H2 D64, against the fp32 reference on the GPU ([S, S] fp32 matrices of
+    the reference, up to 1 GiB each). The odd S = 8191 takes the scalar dpd reduce (S % 4 != 0),
+    S = 16384 the 128-bit one. The kernels' dpd partial rows take B*H*ceil(S/128)*(S+128)*4
+    bytes of workspace, quadratic in S but 1/128 of the reference's [B, H, S, S] dbias."""
+    log(f"relpos long context B1 S{S} H2 D64")
+    qkv, pd, dout, cand = _check(1, S, 2, 64, 0.125, ref_device="cuda")
+    dpd = cand[2]
+    assert (dpd.sum(1).abs() <= 1e-3 * dpd.abs().sum(1) + 1e-4).all()
+
+
 def test_relpos_backward_deterministic():
     log("relpos determinism B2 S512 H4 D64")
     B, S, H, D = 2, 512, 4, 64
