@@ -20,6 +20,8 @@
  *     (rstd, lse, out32, pd, dpd) are always fp32. The *_bf16 entry points are
  *     the same functions with dtype fixed to KRSI_DTYPE_BF16.
  *   - Stateless and reentrant: any host thread may call, ordering is by stream.
+ *     The one exception is krsi_rmsnorm_bwd_noalloc, whose calls share a static
+ *     per-device scratch array (see there).
  */
 #ifndef KRSI_H_
 #define KRSI_H_
@@ -47,7 +49,8 @@ enum krsi_status {
   KRSI_ERR_WORKSPACE = 4,       /* workspace missing or smaller than *_workspace_bytes() */
   KRSI_ERR_UNSUPPORTED = 5,     /* a mode, dtype or head dim this build does not implement */
   KRSI_ERR_LAUNCH = 6,          /* the HIP runtime rejected a kernel launch */
-  KRSI_ERR_BAD_SCALE = 7        /* scale or eps is not finite */
+  KRSI_ERR_BAD_SCALE = 7,       /* scale or eps is not finite */
+  KRSI_ERR_TOO_LARGE = 8        /* beyond the static scratch of a no-allocation entry point */
 };
 
 int krsi_abi_version(void);
@@ -79,6 +82,26 @@ int krsi_rmsnorm_bwd(const void* g, const void* x, const void* w, const float* r
 int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const float* rstd,
                           void* dx, void* dw, void* workspace, size_t workspace_bytes,
                           int64_t rows, int32_t n, void* stream);
+
+/* No counterpart in the reference. It exists for callers that cannot allocate:
+ * code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc. It is krsi_rmsnorm_bwd (same arguments, kernels and bitwise
+ * results) without the workspace arguments. The partial rows go to a static
+ * 16 MiB device array of the library:
+ *   - each GPU holds its own copy from library load until the process ends;
+ *   - the copy used is the current device's (the stream must belong to it);
+ *   - its address is looked up once per device on the first call.
+ * Limit: krsi_rmsnorm_bwd_workspace_bytes(rows, n) <= 16 MiB. That holds for
+ * every row count when n <= 7936, and for fewer rows above that (n = 8192:
+ * rows <= 496). Larger problems return KRSI_ERR_TOO_LARGE before anything is
+ * launched.
+ * Allocates nothing: no hipMalloc, hipFree or allocating library call.
+ * Calls that overlap on one GPU (several streams or host threads) share the
+ * array and race; serialise them. The array keeps the last call's contents.
+ * None of them needs to start at zero. */
+int krsi_rmsnorm_bwd_noalloc(const void* g, const void* x, const void* w, const float* rstd,
+                             void* dx, void* dw, int64_t rows, int32_t n, int32_t dtype,
+                             void* stream);
 
 /* -------------------------------------------------------------------- GEGLU
  * Replaces library/geglu.py:55-61 (_fwd: _geglu_fwd :27-35).

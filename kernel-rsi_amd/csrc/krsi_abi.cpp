@@ -23,6 +23,9 @@ const char* krsi_error_string(int status) {
       return "krsi: the HIP runtime rejected a kernel launch";
     case KRSI_ERR_BAD_SCALE:
       return "krsi: scale or eps is not finite";
+    case KRSI_ERR_TOO_LARGE:
+      return "krsi: the problem needs more scratch than the no-allocation entry point's static "
+             "16 MiB buffer (use the entry point that takes a workspace)";
     default:
       return "krsi: unknown status";
   }

@@ -26,6 +26,7 @@
 #include "krsi_internal.h"
 
 #include <initializer_list>
+#include <mutex>
 
 namespace krsi {
 namespace {
@@ -500,6 +501,33 @@ int rmsnorm_bwd_empty(void* dw, int n, hipStream_t st) {
 
 bool known_dtype(int32_t dt) { return dt == kBf16 || dt == kF16 || dt == kF32; }
 
+// ------------------------------------------------- backward without allocation
+// The partial-row workspace of the backward, as a device array the library owns, for callers
+// that cannot allocate (code under HIP graph capture, serving loops that forbid hipMalloc). Every
+// GPU the library runs on holds its own copy from load until the process ends. In host code the
+// name `scratch` is only a stand-in for the symbol: its device address is looked up once per
+// device with hipGetSymbolAddress, and only that address is ever passed to kernels.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// This device's copy of `scratch` (current device), looked up on its first use.
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return KRSI_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return KRSI_ERR_LAUNCH;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return KRSI_OK;
+}
+
 }  // namespace
 
 }  // namespace krsi
@@ -563,6 +591,21 @@ int krsi_rmsnorm_bwd(const void* g, const void* x, const void* w, const float* r
     default:
       return rmsnorm_bwd<kBf16>(g, x, w, rstd, dx, dw, workspace, rows, n, st);
   }
+}
+
+int krsi_rmsnorm_bwd_noalloc(const void* g, const void* x, const void* w, const float* rstd, void* dx,
+                             void* dw, int64_t rows, int32_t n, int32_t dtype, void* stream) {
+  using namespace krsi;
+  if (!known_dtype(dtype)) return KRSI_ERR_UNSUPPORTED;
+  if (rows < 0 || n <= 0 || n > 16384) return KRSI_ERR_BAD_SHAPE;
+  if (!dw) return KRSI_ERR_NULL_POINTER;
+  if (rows > 0 && (!g || !x || !w || !rstd || !dx)) return KRSI_ERR_NULL_POINTER;
+  const size_t need = krsi_rmsnorm_bwd_workspace_bytes(rows, n);
+  if (need > kScratchBytes) return KRSI_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != KRSI_OK) return rc;
+  return krsi_rmsnorm_bwd(g, x, w, rstd, dx, dw, ws, kScratchBytes, rows, n, dtype, stream);
 }
 
 int krsi_rmsnorm_fwd_bf16(const void* x, const void* w, void* y, float* rstd, int64_t rows,

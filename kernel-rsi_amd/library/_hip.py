@@ -27,6 +27,7 @@ SIGNATURES = {
     "krsi_rmsnorm_bwd_workspace_bytes": (_SZ, [_I64, _I32]),
     "krsi_rmsnorm_bwd": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I32, _I32, _P]),
     "krsi_rmsnorm_bwd_bf16": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I32, _P]),
+    "krsi_rmsnorm_bwd_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _P]),
     "krsi_geglu_fwd": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P]),
     "krsi_geglu_fwd_bf16": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P]),
     "krsi_geglu_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _I32, _P]),

@@ -41,7 +41,7 @@ def test_single_hip_runtime_in_process():
 
 def test_error_strings():
     lib = _hip.lib()
-    for code in range(0, 8):
+    for code in range(0, 9):
         s = lib.krsi_error_string(code).decode()
         assert s and ("krsi" in s or code == 0)
     assert "unknown" in lib.krsi_error_string(99).decode()
@@ -96,6 +96,28 @@ def test_validation_before_launch():
                                     2, 16, 2, 64, 0.125, NULL) == E["WS"]
     assert lib.krsi_relpos_bwd_bf16(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 200, FAKE, FAKE, ws,
                                     2, 16, 2, 64, 0.125, NULL) == E["SHAPE"]
+
+
+def test_noalloc_backward_validates_before_touching_the_device():
+    """krsi_rmsnorm_bwd_noalloc checks its arguments, and that the problem fits its static
+    16 MiB scratch, before any HIP call (FAKE pointers: nothing is dereferenced)."""
+    lib = _hip.lib()
+    f = lib.krsi_rmsnorm_bwd_noalloc
+    TOO_LARGE = 8
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 0, 0, NULL) == 2          # n = 0
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 16385, 0, NULL) == 2      # n above 16384
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 7, NULL) == 5         # unknown dtype
+    assert f(FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 4, 64, 0, NULL) == 1         # dw NULL
+    assert f(NULL, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 0, NULL) == 1         # g NULL
+    limit = 16 << 20
+    for rows, n in ((32768, 8192), (1 << 20, 16384), (497, 8192)):
+        assert lib.krsi_rmsnorm_bwd_workspace_bytes(rows, n) > limit
+        for dt in (0, 1, 2):
+            assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, rows, n, dt, NULL) == TOO_LARGE
+    # The stated limit: every row count fits for n <= 7936, and n = 8192 fits up to 496 rows.
+    for rows, n in ((1 << 24, 7936), (496, 8192), (32768, 4096)):
+        assert lib.krsi_rmsnorm_bwd_workspace_bytes(rows, n) <= limit
+    assert "16 MiB" in lib.krsi_error_string(TOO_LARGE).decode()
 
 
 def test_dtype_argument_validated_before_launch():
