@@ -35,8 +35,8 @@ extern "C" {
 
 #define KRSI_ABI_VERSION 2
 
-/* Activation dtypes. The reference's Triton kernels are dtype-generic; the
- * attention entry points take bf16 and fp16 (fp32 qkv: KRSI_ERR_UNSUPPORTED). */
+/* Activation dtypes. The reference's Triton kernels are dtype-generic, and so is
+ * every entry point here. */
 #define KRSI_DTYPE_BF16 0
 #define KRSI_DTYPE_F16 1
 #define KRSI_DTYPE_F32 2
@@ -125,15 +125,18 @@ int krsi_geglu_bwd_bf16(const void* g, const void* u, void* du, int64_t rows, in
 
 /* ------------------------------------------------- relative-position attention
  * Replaces library/relpos_attention.py:132-140 (_forward: _fwd :26-59).
- * dtype: KRSI_DTYPE_BF16 or KRSI_DTYPE_F16 (T); P is rounded to T before the
- * P V product, as the reference rounds it to v's dtype (:53).
+ * dtype (T): KRSI_DTYPE_BF16 or KRSI_DTYPE_F16 run on 16-bit MFMA, and P is rounded
+ * to T before the P V product, as the reference rounds it to v's dtype (:53).
+ * KRSI_DTYPE_F32 runs on fp32 MFMA with every product in fp32. P is not
+ * rounded, since v's dtype is fp32.
  * qkv: [B*S, ld_qkv] of T, unit column stride; token t = b*S + s holds
  *      q at columns [h*D, h*D+D), k at [H*D + h*D, ...), v at [2*H*D + h*D, ...).
  * pd:  [H, 2S-1] fp32, bias[h,i,j] = pd[h, j - i + S - 1].
  * out: [B*S, H*D] of T; out32: same, fp32; lse: [B*H, S] fp32 in the log2
  *      domain (lse = log2 sum_j 2^{(q.k*scale + bias) * log2(e)}).
- * Limits: D % 8 == 0 and 8 <= D <= 128, ld_qkv % 8 == 0, ld_qkv >= 3*H*D,
- *         S >= 1, S * ld_qkv * 2 < 2^31 bytes (UNSUPPORTED otherwise),
+ * Limits: D % 8 == 0 and 8 <= D <= 128, ld_qkv >= 3*H*D, rows of a multiple
+ *         of 16 bytes (ld_qkv % 8 == 0 for 16-bit T, % 4 for fp32), S >= 1,
+ *         and for 16-bit T S * ld_qkv * 2 < 2^31 bytes (UNSUPPORTED otherwise),
  *         scale finite, and scale == 0 or |scale| * log2(e) >= 2^-60
  *         (BAD_SCALE otherwise: the bias is folded into the score accumulator
  *         as pd * log2(e) / |scale * log2(e)|). Non-causal.                  */
@@ -150,7 +153,8 @@ int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void*
  * diagonals j - i, into per-block partials summed in a fixed order.
  * dout: [B*S, H*D] of T contiguous; dqkv: [B*S, ld_dqkv] of T (same column
  * layout as qkv, every q/k/v column written); dpd: [H, 2S-1] fp32 (overwritten).
- * P and dS are rounded to T before their products (:88-92, :125).
+ * P and dS are rounded to T before their products (:88-92, :125); for fp32
+ * that is no rounding. ld_dqkv rows are a multiple of 16 bytes too.
  * workspace: at least krsi_relpos_bwd_workspace_bytes(B,S,H,D) bytes.        */
 size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t D);
 int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,

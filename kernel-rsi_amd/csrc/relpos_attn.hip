@@ -62,6 +62,7 @@
 
 #include "krsi_device.h"
 #include "krsi_internal.h"
+#include "relpos_common.h"
 
 namespace krsi {
 namespace {
@@ -73,7 +74,6 @@ constexpr std::integral_constant<int, 0> kBuf0{};
 constexpr std::integral_constant<int, 1> kBuf1{};
 constexpr std::integral_constant<bool, false> kFull{};
 constexpr std::integral_constant<bool, true> kTail{};
-constexpr float kLog2e = 1.4426950408889634f;
 
 template <int DP>
 struct Geo {
@@ -354,16 +354,6 @@ __device__ __forceinline__ f32x16 read_bias16(const float* bw, int x0) {
     for (int b = 0; b < 4; ++b) out[4 * a + b] = v[b];
   }
   return out;
-}
-
-// Tile of a 1-D grid of N = (blocks per head) x (B*H) workgroups. Workgroups are handed
-// to the 8 XCDs round-robin by linear id and every XCD has its own L2, so XCD x gets the
-// contiguous tile range [x N/8, (x+1) N/8) in order: the blocks of one (batch, head) run
-// on one XCD at about the same time and share its streamed K/V (or Q/dO) tiles in L2.
-constexpr int kXcds = 8;
-__device__ __forceinline__ int xcd_tile(int w, int N) {
-  const int x = w % kXcds, k = w / kXcds, q = N / kXcds, r = N % kXcds;
-  return x * q + min(x, r) + k;
 }
 
 // The forward's row sum l: of the fp32 p, as the reference (relpos_attention.py:51), or of
@@ -1251,14 +1241,16 @@ constexpr int kDkdvNW = 4;
 // stay finite for any realistic table.
 constexpr float kMinScaleLog2 = 8.67361737988403547e-19f;  // 2^-60
 
-int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float scale) {
+// esize: bytes per activation element (2 for bf16 / fp16, 4 for fp32).
+int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float scale, int esize) {
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return KRSI_ERR_BAD_SHAPE;
   if (D % 8 != 0 || D > 128) return KRSI_ERR_UNSUPPORTED;
   if ((int64_t)B * H > 65535 || S > (1 << 24)) return KRSI_ERR_BAD_SHAPE;
   if (ld < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
-  // Buffer resources of one (batch, head) slice hold S rows of ld 16-bit values in < 2^31 bytes.
-  if ((int64_t)S * ld * 2 >= ((int64_t)1 << 31)) return KRSI_ERR_UNSUPPORTED;
-  if (ld % 8 != 0 || !aligned16(qkv)) return KRSI_ERR_MISALIGNED;
+  // The 16-bit kernels' buffer resources of one (batch, head) slice hold S rows of ld values
+  // in < 2^31 bytes (the fp32 kernels address with 64-bit offsets).
+  if (esize == 2 && (int64_t)S * ld * 2 >= ((int64_t)1 << 31)) return KRSI_ERR_UNSUPPORTED;
+  if ((ld * esize) % 16 != 0 || !aligned16(qkv)) return KRSI_ERR_MISALIGNED;
   if (!(scale == scale) || scale > 3.0e38f || scale < -3.0e38f) return KRSI_ERR_BAD_SCALE;
   const float c = fabsf(scale * kLog2e);
   if (c != 0.f && c < kMinScaleLog2) return KRSI_ERR_BAD_SCALE;
@@ -1274,7 +1266,7 @@ Fold fold_scale(float scale) {
 
 int padded_dim(int D) { return (D + 15) / 16 * 16; }
 
-constexpr int kKvRows = Blk<kDkdvNW>::ROWS;
+static_assert(Blk<kDkdvNW>::ROWS == kKvRows, "dpd partial rows: one per kKvRows keys");
 
 size_t ws_delta_bytes(int B, int S, int H) { return align256((size_t)B * H * S * sizeof(float)); }
 // One dpd partial row of S + rows floats per (b, h, key block).
@@ -1313,15 +1305,7 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DT, DP, kDkdvNW>), dim3((unsigned)(nkb * B * H)),
                      dim3(KK::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
                      (const float*)delta, (uint16_t*)dqkv, ldd, part, S, H, D, f, scale);
-  if (S % 4 == 0) {
-    const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 256), (unsigned)H);
-    hipLaunchKernelGGL(relpos_dpd_reduce4, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S,
-                       H, nkb, KK::ROWS);
-  } else {
-    const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
-    hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, (const float*)part, dpd, B, S, H,
-                       nkb, KK::ROWS);
-  }
+  launch_dpd_reduce(part, dpd, B, S, H, st);
 }
 
 template <int DT>
@@ -1361,6 +1345,18 @@ int dispatch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd,
 }
 
 }  // namespace
+
+void launch_dpd_reduce(const float* part, float* dpd, int B, int S, int H, hipStream_t st) {
+  const int nkb = (int)ceil_div(S, kKvRows);
+  if (S % 4 == 0) {
+    const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 256), (unsigned)H);
+    hipLaunchKernelGGL(relpos_dpd_reduce4, rgrid, dim3(256), 0, st, part, dpd, B, S, H, nkb, kKvRows);
+  } else {
+    const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
+    hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, part, dpd, B, S, H, nkb, kKvRows);
+  }
+}
+
 }  // namespace krsi
 
 extern "C" {
@@ -1369,13 +1365,16 @@ int krsi_relpos_fwd(const void* qkv, int64_t ld_qkv, const float* pd, void* out,
                     float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
                     int32_t dtype, void* stream) {
   using namespace krsi;
-  if (dtype != kBf16 && dtype != kF16) return KRSI_ERR_UNSUPPORTED;
+  if (dtype != kBf16 && dtype != kF16 && dtype != kF32) return KRSI_ERR_UNSUPPORTED;
   if (!qkv || !pd || !out || !out32 || !lse) return KRSI_ERR_NULL_POINTER;
-  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
+  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale, dtype == kF32 ? 4 : 2);
   if (rc != KRSI_OK) return rc;
   if (!aligned16(out) || !aligned16(out32)) return KRSI_ERR_MISALIGNED;
-  const Fold f = fold_scale(scale);
   hipStream_t st = as_stream(stream);
+  if (dtype == kF32)
+    return relpos_fwd_f32(static_cast<const float*>(qkv), ld_qkv, pd, static_cast<float*>(out), out32, lse,
+                          B, S, H, D, scale, st);
+  const Fold f = fold_scale(scale);
   return dtype == kF16 ? dispatch_fwd<kF16>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, f, st)
                        : dispatch_fwd<kBf16>(qkv, ld_qkv, pd, out, out32, lse, B, S, H, D, f, st);
 }
@@ -1399,18 +1398,25 @@ int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const flo
                     void* workspace, size_t workspace_bytes, int32_t B, int32_t S, int32_t H,
                     int32_t D, float scale, int32_t dtype, void* stream) {
   using namespace krsi;
-  if (dtype != kBf16 && dtype != kF16) return KRSI_ERR_UNSUPPORTED;
+  if (dtype != kBf16 && dtype != kF16 && dtype != kF32) return KRSI_ERR_UNSUPPORTED;
   if (!dout || !qkv || !pd || !out32 || !lse || !dqkv || !dpd) return KRSI_ERR_NULL_POINTER;
-  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale);
+  const int esize = dtype == kF32 ? 4 : 2;
+  int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale, esize);
   if (rc != KRSI_OK) return rc;
   if (ld_dqkv < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
-  if (ld_dqkv % 8 != 0 || !aligned16(dqkv) || !aligned16(dout) || !aligned16(out32))
+  if ((ld_dqkv * esize) % 16 != 0 || !aligned16(dqkv) || !aligned16(dout) || !aligned16(out32))
     return KRSI_ERR_MISALIGNED;
   if (!workspace || workspace_bytes < krsi_relpos_bwd_workspace_bytes(B, S, H, D))
     return KRSI_ERR_WORKSPACE;
   if (!aligned16(workspace)) return KRSI_ERR_MISALIGNED;
-  const Fold f = fold_scale(scale);
   hipStream_t st = as_stream(stream);
+  if (dtype == kF32) {
+    float* delta = static_cast<float*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws_delta_bytes(B, S, H));
+    return relpos_bwd_f32(static_cast<const float*>(dout), static_cast<const float*>(qkv), ld_qkv, pd, out32,
+                          lse, static_cast<float*>(dqkv), ld_dqkv, dpd, delta, part, B, S, H, D, scale, st);
+  }
+  const Fold f = fold_scale(scale);
   return dtype == kF16
              ? dispatch_bwd<kF16>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace,
                                   B, S, H, D, f, scale, st)

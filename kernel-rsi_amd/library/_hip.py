@@ -45,7 +45,7 @@ SIGNATURES = {
 
 # KRSI_DTYPE_* codes of the activation dtypes.
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
-_ATTN_DTYPES = (torch.bfloat16, torch.float16)
+_ATTN_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 _lib = None
 _lock = threading.Lock()

@@ -198,10 +198,12 @@ def diag_sum(ds: torch.Tensor, S: int) -> torch.Tensor:
     return out.index_add_(1, idx, ds.reshape(H, S * S))
 
 
-def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False, eager_dtype=None):
-    """Forward and backward of the reference in explicit fp32 math with contiguous matmul
-    operands (device-agnostic; no 16-bit batched product is ever formed).
-      no eager dtype : the fp32 reference (ref32) of the (16-bit) inputs.
+def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False, eager_dtype=None,
+                  compute_dtype=torch.float32):
+    """Forward and backward of the reference in explicit math with contiguous matmul operands
+    (device-agnostic; no 16-bit batched product is ever formed), in compute_dtype (fp32, or
+    float64 for the reference of fp32 inputs).
+      no eager dtype : the reference (ref32) of the inputs.
       eager_dtype=T  : the eager original in dtype T (bf16 or fp16) as torch runs it -
                        SDPA-MATH upcasts 16-bit inputs to fp32 internally, so it is this fp32
                        math with the bias rounded to T (relpos_attention.py:207), out and dqkv
@@ -210,8 +212,9 @@ def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False, eager_dtyp
     Returns (out [B*S, H*D], lse [B*H, S] log2 domain, dqkv [B*S, 3*H*D], dpd [H, 2S-1])."""
     if eager_bf16:
         eager_dtype = torch.bfloat16
-    q, k, v = (t.float().contiguous() for t in split_qkv(qkv, B, S, H, D))
-    bias = bias_matrix(pd.float(), S)[None]
+    cdt = compute_dtype
+    q, k, v = (t.to(cdt).contiguous() for t in split_qkv(qkv, B, S, H, D))
+    bias = bias_matrix(pd.to(cdt), S)[None]
     if eager_dtype is not None:
         bias = bias.to(eager_dtype).float()
     s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * scale + bias
@@ -219,7 +222,7 @@ def relpos_manual(qkv, pd, B, S, H, D, scale, dout, eager_bf16=False, eager_dtyp
     p = torch.exp(s - lse[..., None])
     del s
     o = torch.matmul(p, v)
-    do = dout.float().reshape(B, S, H, D).permute(0, 2, 1, 3).contiguous()
+    do = dout.to(cdt).reshape(B, S, H, D).permute(0, 2, 1, 3).contiguous()
     dp = torch.matmul(do, v.transpose(-2, -1).contiguous())
     delta = (do * o).sum(-1, keepdim=True)
     ds = p * (dp - delta)

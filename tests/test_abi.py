@@ -130,7 +130,7 @@ def test_dtype_argument_validated_before_launch():
         assert lib.krsi_rmsnorm_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, 4, 64, dt, NULL) == UNSUP
         assert lib.krsi_geglu_fwd(FAKE, FAKE, 4, 8, 1, dt, NULL) == UNSUP
         assert lib.krsi_geglu_bwd(FAKE, FAKE, FAKE, 4, 8, 1, dt, NULL) == UNSUP
-    for dt in (2, 3):
+    for dt in (3, -1):
         assert lib.krsi_relpos_fwd(FAKE, 384, FAKE, FAKE, FAKE, FAKE, 2, 16, 2, 64, 0.125, dt, NULL) == UNSUP
         assert lib.krsi_relpos_bwd(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 384, FAKE, FAKE, 1 << 30,
                                    2, 16, 2, 64, 0.125, dt, NULL) == UNSUP
@@ -138,8 +138,14 @@ def test_dtype_argument_validated_before_launch():
     for dt in (0, 1, 2):
         assert lib.krsi_rmsnorm_fwd(NULL, FAKE, FAKE, FAKE, 4, 64, 1e-6, dt, NULL) == NULLP
         assert lib.krsi_geglu_fwd(NULL, FAKE, 4, 8, 1, dt, NULL) == NULLP
-    for dt in (0, 1):
+    for dt in (0, 1, 2):
         assert lib.krsi_relpos_fwd(FAKE, 384, NULL, FAKE, FAKE, FAKE, 2, 16, 2, 64, 0.125, dt, NULL) == NULLP
+    # fp32 qkv rows need a 16-byte multiple (ld % 4); 16-bit rows ld % 8. The 2^31-byte slice
+    # limit of the 16-bit kernels' buffer resources does not apply to fp32.
+    ALIGN = 3
+    assert lib.krsi_relpos_fwd(FAKE, 386, FAKE, FAKE, FAKE, FAKE, 2, 16, 2, 64, 0.125, 2, NULL) == ALIGN
+    assert lib.krsi_relpos_fwd(FAKE, 388, FAKE, FAKE, FAKE, FAKE, 2, 16, 2, 64, 0.125, 0, NULL) == ALIGN
+    assert lib.krsi_relpos_fwd(FAKE, 1024, FAKE, FAKE, FAKE, FAKE, 1, 1 << 20, 2, 64, 0.125, 0, NULL) == UNSUP
     # The workspace size does not depend on the dtype: one size serves all three.
     assert lib.krsi_rmsnorm_bwd_workspace_bytes(1000, 16384) >= 512 * 16384 * 4
     assert _hip.DTYPE_CODES == {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}

@@ -6,7 +6,11 @@ Tolerance, stated: the reference's acceptance criterion with slack 2 (tools/comm
 eager original in the same dtype, per-row errors within 3x, with the criterion's absolute
 floors (1e-3 of the peak per element, 1e-5 rel-L2), which is what an fp32 run is held to.
 Attention in fp16 is additionally held to the reference Triton kernels' own rounding points
-(P and dS rounded to fp16), per row at 3x. fp32 attention is not implemented and must raise.
+(P and dS rounded to fp16), per row at 3x. Attention in fp32 (fp32 MFMA, P and dS unrounded as
+the reference keeps them for fp32 inputs) is held to the same criterion against a float64
+reference of the same fp32 inputs, with the eager fp32 computation as the yardstick; in practice
+that is the floors (1e-5 rel-L2, 1e-3 of the peak per element, per-row 3x the median row error
++ 1e-5), far tighter than the reference's own fp32 path, which runs its products in TF32.
 """
 import math
 
@@ -159,11 +163,88 @@ def test_relpos_fp16_strided_and_large():
     _relpos_fp16(2, 1024, 16, 72, 1 / math.sqrt(72), ref_device="cuda")
 
 
-def test_relpos_fp32_rejected():
-    qkv = torch.zeros(8, 3 * 2 * 16, device="cuda", dtype=torch.float32)
-    pd = torch.zeros(2, 7, device="cuda", dtype=torch.float32)
-    with pytest.raises(TypeError):
-        A.relpos_attention(qkv, pd, 2, 4, 2, 16, 0.25)
+def _relpos_fp32(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_extra=0, seed=70):
+    dt = torch.float32
+    qkv = seeded((B * S, 3 * H * D + ld_extra), seed, std=std, dtype=dt)
+    if ld_extra:
+        qkv = qkv[:, :3 * H * D]
+    pd = seeded((H, 2 * S - 1), seed + 1, std=pd_std, dtype=torch.float32)
+    dout = seeded((B * S, H * D), seed + 2, dtype=dt)
+    x = qkv.detach().requires_grad_(True)
+    p = pd.detach().requires_grad_(True)
+    out = A.relpos_attention(x, p, B, S, H, D, scale)
+    dqkv, dpd = torch.autograd.grad(out, [x, p], dout)
+    assert out.dtype == dt and dqkv.dtype == dt and dpd.dtype == torch.float32
+    dev = torch.device(ref_device)
+    a = (qkv.to(dev), pd.to(dev), B, S, H, D, scale, dout.to(dev))
+    r = O.relpos_manual(*a, compute_dtype=torch.float64)
+    o = O.relpos_manual(*a)  # the eager fp32 computation (explicit fp32 matmuls + softmax)
+    cand = (out.detach().to(dev), dqkv.to(dev), dpd.to(dev))
+    tag = f"fp32 B{B} S{S} H{H} D{D}"
+    assert_parity(["out", "dqkv", "dpd"], (r[0], r[2], r[3]), (o[0], o[2], o[3]), cand,
+                  extra_msg=tag + " vs eager fp32")
+    _, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, scale)
+    assert torch.equal(out32, out.detach())
+    assert torch.allclose(lse.to(dev).double(), r[1], atol=1e-5, rtol=1e-6), (lse.to(dev) - r[1]).abs().max()
+
+
+FP32_CASES = [  # B, S, H, D, scale, qkv std, pd std
+    (1, 2, 1, 64, 0.125, 1.0, 0.02),
+    (1, 17, 2, 32, 0.2, 1.0, 1.0),
+    (2, 64, 2, 64, 1.0, 0.6, 1.0),
+    (1, 128, 2, 128, 1 / math.sqrt(128), 1.0, 0.02),
+    (2, 300, 2, 72, 1 / math.sqrt(72), 1.0, 0.02),
+    (1, 200, 1, 16, 0.25, 1.0, 0.5),
+    (1, 130, 2, 48, 0.3, 1.0, 0.02),
+    (1, 100, 1, 80, 0.1, 1.0, 0.02),
+    (1, 96, 2, 96, 0.1, 1.0, 0.02),
+    (1, 70, 1, 112, 0.1, 1.0, 0.02),
+    (1, 257, 1, 8, 0.35, 1.0, 0.3),
+    (1, 96, 2, 64, -0.125, 1.0, 0.5),
+    (1, 80, 2, 32, 0.0, 1.0, 1.0),
+]
+
+
+@pytest.mark.parametrize("B,S,H,D,scale,std,pd_std", FP32_CASES)
+def test_relpos_fp32(B, S, H, D, scale, std, pd_std):
+    log(f"relpos fp32 B{B} S{S} H{H} D{D} scale {scale:.4g}")
+    _relpos_fp32(B, S, H, D, scale, std, pd_std)
+
+
+def test_relpos_fp32_single_position():
+    """S = 1: out = v and dv = dout exactly (p = 1 in both passes); dq, dk and dpd are 0 up to
+    the rounding of dp - delta, whose two dot products are summed in different orders."""
+    B, S, H, D = 2, 1, 3, 64
+    qkv = seeded((B * S, 3 * H * D), 80, dtype=torch.float32)
+    pd = seeded((H, 1), 81, dtype=torch.float32)
+    dout = seeded((B * S, H * D), 82, dtype=torch.float32)
+    x = qkv.detach().requires_grad_(True)
+    p = pd.detach().requires_grad_(True)
+    out = A.relpos_attention(x, p, B, S, H, D, 0.125)
+    dqkv, dpd = torch.autograd.grad(out, [x, p], dout)
+    q, k, v = O.split_qkv(qkv, B, S, H, D)
+    assert torch.equal(out.detach(), v.permute(0, 2, 1, 3).reshape(B * S, H * D))
+    d = dqkv.view(B * S, 3, H * D)
+    assert torch.equal(d[:, 2], dout)
+    assert d[:, :2].abs().max().item() < 1e-5 and dpd.abs().max().item() < 1e-5
+
+
+def test_relpos_fp32_strided_and_config4_shape():
+    """A qkv row stride wider than 3*H*D, then the BASELINE config 4 shape (B2 H16 L1024 D72)
+    forward and backward against the float64 reference on the GPU; the backward is bitwise
+    reproducible."""
+    log("relpos fp32 strided qkv B2 S96 H2 D64")
+    _relpos_fp32(2, 96, 2, 64, 0.125, ld_extra=40)
+    log("relpos fp32 B2 S1024 H16 D72 (config 4 shape)")
+    _relpos_fp32(2, 1024, 16, 72, 1 / math.sqrt(72), ref_device="cuda")
+    B, S, H, D = 2, 1024, 16, 72
+    qkv = seeded((B * S, 3 * H * D), 90, dtype=torch.float32)
+    pd = seeded((H, 2 * S - 1), 91, std=0.02, dtype=torch.float32)
+    dout = seeded((B * S, H * D), 92, dtype=torch.float32)
+    _, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, 0.1)
+    a = _hip.relpos_bwd(dout, qkv, pd, out32, lse, B, S, H, D, 0.1)
+    b = _hip.relpos_bwd(dout, qkv, pd, out32, lse, B, S, H, D, 0.1)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
 def test_relpos_fp16_config5_shape():

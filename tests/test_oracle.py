@@ -75,6 +75,22 @@ def test_relpos_manual_fp32_matches_closed_form():
 
 
 # ---------------------------------------------------------------- gradcheck
+def test_relpos_manual_float64_matches_closed_form():
+    """The float64 mode of relpos_manual (the reference of fp32 attention inputs) against the
+    golden float64 closed form, to float64 precision."""
+    g = load("relpos.npz")
+    B, S, H, D = (int(v) for v in g["dims"])
+    m = O.relpos_manual(t64(g["qkv"]), t64(g["pd"]), B, S, H, D, float(g["scale"]), t64(g["dout"]),
+                        compute_dtype=torch.float64)
+    assert all(t.dtype == torch.float64 for t in m)
+    for a, k in ((m[0], "out"), (m[1], "lse"), (m[2], "dqkv"), (m[3], "dpd")):
+        np.testing.assert_allclose(a.numpy(), g[k], rtol=1e-10, atol=1e-12)
+    # A planted mistake must fail: a transposed bias (pd indexed by i - j).
+    flipped = O.relpos_manual(t64(g["qkv"]), t64(g["pd"]).flip(1), B, S, H, D, float(g["scale"]),
+                              t64(g["dout"]), compute_dtype=torch.float64)
+    assert not np.allclose(flipped[0].numpy(), g["out"], rtol=1e-6, atol=1e-8)
+
+
 def test_gradcheck_fp64():
     gen = torch.Generator().manual_seed(7)
     x = torch.randn(3, 10, generator=gen, dtype=torch.float64, requires_grad=True)
