@@ -22,6 +22,9 @@ CSRC = HERE / "csrc"
 INCLUDE = ROOT / "include"
 OBJDIR = HERE / "_build"
 LIB = HERE / "libkrsi_hip.so"
+# The streaming-bandwidth probe of hw.py: its own library, not part of the kernel library.
+PROBE_SRC = HERE / "probe" / "stream_probe.hip"
+PROBE_LIB = HERE / "libkrsi_probe.so"
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code (they are not
@@ -80,6 +83,9 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([hipcc, *HIP_FLAGS, "-shared", "-o", str(tmp), str(PROBE_SRC)], verbose)
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 

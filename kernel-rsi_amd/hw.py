@@ -1,13 +1,15 @@
 #!/usr/bin/env python3
 """Measured ceilings of this GPU, written to hardware/<gpu>.json.
 
-  python kernel-rsi_amd/hw.py [--quick]
+  python kernel-rsi_amd/hw.py [--quick] [--stream-only]
 
 The reference's tools read two things from such a record: `tflops[dtype]` and
 `bw_copy_gbs` / `bw_read_gbs` (tools/common.py:56-64; its own probe is tools/hw.py). They use
 them as roofline denominators. This module fills those keys for an MI355X and adds what this
 package's roofline discussion uses:
   * the published peaks;
+  * the rate of a hand-written streaming kernel at each read:write mix (libkrsi_probe.so), the
+    practical HBM ceiling for bandwidth-bound kernels, which torch's copy does not reach;
   * launch costs;
   * the ridge points.
 The probes are a table of small functions. Each runs under `Clock`, which reports the median
@@ -122,6 +124,56 @@ def probe_bandwidth(clock: Clock) -> dict:
     return {k: round(v) for k, v in res.items()}
 
 
+STREAM_MIXES = ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (3, 2))
+
+
+def probe_stream(clock: Clock, quick: bool = False) -> dict:
+    """GB/s of a hand-written streaming kernel (libkrsi_probe.so, built with the library) at each
+    read:write mix, cache-cold. This is the practical HBM ceiling for bandwidth-bound kernels
+    moving bytes in that proportion (RMSNorm forward is 1:1, its backward and the GEGLU forward
+    2:1, the GEGLU backward 3:2). Best over a small sweep of grid size, chunks in flight and
+    non-temporal stores. Each array is 512 MiB; two sets alternate, so no call finds its data in
+    the 256 MB MALL."""
+    import ctypes
+
+    path = HERE / "libkrsi_probe.so"
+    if not path.is_file():
+        return {"error": f"{path.name} not built"}
+    lib = ctypes.CDLL(str(path))
+    lib.krsi_probe_stream.restype = ctypes.c_int
+    lib.krsi_probe_stream.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                                           ctypes.c_void_p]
+    nbytes = 512 << 20
+    n = nbytes // 16
+    sets = [[torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 256) for _ in range(5)]
+            for _ in range(2)]
+    ptrs = [(ctypes.c_void_p * 3)(*[t.data_ptr() for t in s[:3]]) for s in sets]
+    outs = [(ctypes.c_void_p * 2)(*[t.data_ptr() for t in s[3:]]) for s in sets]
+    stream = torch.cuda.current_stream().cuda_stream
+    sweep = [(u, nt, b) for u in (1, 4) for nt in (0, 1) for b in ((1024, 32768) if quick else (1024, 4096, 32768))]
+    res = {}
+    for r, w in STREAM_MIXES:
+        best = (0.0, None)
+        for u, nt, blocks in sweep:
+            if w == 0 and nt:
+                continue
+            k = [0]
+
+            def call():
+                i = k[0] % 2
+                k[0] += 1
+                rc = lib.krsi_probe_stream(r, w, u, nt, blocks, ptrs[i], outs[i], n, stream)
+                if rc:
+                    raise RuntimeError(f"krsi_probe_stream({r}, {w}, {u}, {nt}, {blocks}) returned {rc}")
+            gbs = (r + w) * nbytes / clock.ms(call, 4) / 1e6
+            if gbs > best[0]:
+                best = (gbs, {"unroll": u, "nontemporal": nt, "blocks": blocks})
+        res[f"r{r}w{w}"] = {"gbs": round(best[0]), **best[1]}
+    del sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def probe_launch(clock: Clock) -> dict:
     """Microseconds per tiny kernel: one stream launch of a torch op, one graph replay."""
     x = torch.zeros(1, device="cuda")
@@ -149,6 +201,7 @@ def collect(quick: bool = False) -> dict:
            "l2_mb": round(getattr(props, "L2_cache_size", 0) / 2 ** 20, 1),
            "memory_gb": round(props.total_memory / 2 ** 30, 1), "tflops": tflops}
     rec.update(probe_bandwidth(clock))
+    rec["stream_kernel_gbs"] = probe_stream(clock, quick)
     stream_bw = max(rec["bw_copy_gbs"], rec["bw_read_gbs"])
     rec["ridge_flop_per_byte"] = {k: round(v * 1e3 / stream_bw, 1) for k, v in tflops.items()
                                   if isinstance(v, (int, float))}
@@ -177,9 +230,15 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--quick", action="store_true", help="smaller GEMM and fewer samples")
     ap.add_argument("--out-dir", type=Path, default=HERE / "hardware", help="where the record goes")
+    ap.add_argument("--stream-only", action="store_true",
+                    help="only the streaming-kernel ceilings, printed, no record written")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("hw.py measures a GPU; none is visible")
+    if args.stream_only:
+        for mix, v in probe_stream(Clock(samples=5), args.quick).items():
+            print(f"{mix}: {v}", flush=True)
+        return 0
     rec = collect(args.quick)
     width = max(map(len, rec))
     for k, v in rec.items():
