@@ -37,7 +37,7 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
-sys.path[:0] = [str(ROOT / "kernel-rsi_amd" / "library"), str(ROOT / "oracle")]
+sys.path[:0] = [str(ROOT / "kernel-rsi_amd" / "library"), str(ROOT / "kernel-rsi_amd"), str(ROOT / "oracle")]
 
 import torch  # noqa: E402
 
@@ -430,6 +430,35 @@ def bench_config1(args) -> dict:
     return {"workload": "rmsnorm fwd on the reference's CPU path, eps 1e-6 (BASELINE config 1)", "shapes": res}
 
 
+# ------------------------------------------------------- measured HBM ceiling
+# Read:write byte mix of each bandwidth-bound kernel (algorithmic bytes).
+KERNEL_MIX = {"rmsnorm_fwd": (1, 1), "rmsnorm_bwd": (2, 1), "geglu_fwd": (2, 1), "geglu_bwd": (3, 2)}
+
+
+def attach_stream_ceiling(comps: dict) -> dict:
+    """The cache-cold rate of a plain streaming kernel at each kernel's read:write mix on this
+    box (hw.py's probe). Each bandwidth component gets the ceiling of its fwd+bwd step (the
+    probe's time for the same bytes at the same mixes) and its fraction of it, beside the
+    roofline against the published 8 TB/s."""
+    import hw
+    wanted = sorted({KERNEL_MIX[k] for c in comps.values() for k in c.get("kernels", {}) if k in KERNEL_MIX})
+    if not wanted:
+        return {}
+    probe = hw.probe_stream(hw.Clock(samples=3), quick=True, mixes=wanted)
+    if "error" in probe:
+        return probe
+    gbs = {mix: probe[f"r{mix[0]}w{mix[1]}"]["gbs"] for mix in wanted}
+    for comp in comps.values():
+        ks = {k: v for k, v in comp.get("kernels", {}).items() if k in KERNEL_MIX}
+        if not ks:
+            continue
+        t = sum(v["bytes"] / (gbs[KERNEL_MIX[k]] * 1e9) for k, v in ks.items())
+        ceil = sum(v["bytes"] for v in ks.values()) / t / 1e9
+        comp["stream_ceiling"] = {"GB/s": round(ceil, 1), "frac": round(comp["value"] / ceil, 4),
+                                  "source": "hw.py streaming probe at each kernel's read:write mix, this run"}
+    return {f"stream_r{r}w{w}_GB/s": v for (r, w), v in gbs.items()}
+
+
 # ------------------------------------------------------------------- traffic
 def _csrc_sha256() -> str:
     import hashlib
@@ -517,6 +546,7 @@ def main() -> None:
     if "config1" in only:
         comps["rmsnorm_config1"] = bench_config1(args)
     attach_traffic(comps)
+    ceilings = attach_stream_ceiling(comps)
     head = comps.get("relpos_attention") or next(c for c in comps.values() if "value" in c)
     cpu = cpu_model()
     line = {
@@ -528,7 +558,7 @@ def main() -> None:
         "cpu_baseline": {**head["cpu_baseline"], "cpu": cpu["model"]} if "cpu_baseline" in head else None,
         "components": comps,
         "host_cpu": cpu,
-        "measured_peaks": {"hbm_copy_GB/s": measured_copy_gbs()},
+        "measured_peaks": {"hbm_copy_GB/s (torch copy)": measured_copy_gbs(), **ceilings},
     }
     print(json.dumps(line))
 

@@ -127,7 +127,7 @@ def probe_bandwidth(clock: Clock) -> dict:
 STREAM_MIXES = ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (3, 2))
 
 
-def probe_stream(clock: Clock, quick: bool = False) -> dict:
+def probe_stream(clock: Clock, quick: bool = False, mixes=STREAM_MIXES) -> dict:
     """GB/s of a hand-written streaming kernel (libkrsi_probe.so, built with the library) at each
     read:write mix, cache-cold. This is the practical HBM ceiling for bandwidth-bound kernels
     moving bytes in that proportion (RMSNorm forward is 1:1, its backward and the GEGLU forward
@@ -152,7 +152,7 @@ def probe_stream(clock: Clock, quick: bool = False) -> dict:
     stream = torch.cuda.current_stream().cuda_stream
     sweep = [(u, nt, b) for u in (1, 4) for nt in (0, 1) for b in ((1024, 32768) if quick else (1024, 4096, 32768))]
     res = {}
-    for r, w in STREAM_MIXES:
+    for r, w in mixes:
         best = (0.0, None)
         for u, nt, blocks in sweep:
             if w == 0 and nt:
