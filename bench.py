@@ -7,8 +7,8 @@ timed on the host CPU beside it.
 
     python bench.py [--steps K] [--warmup W] [--only LIST] [--no-cpu] [--cpu-seconds S]
 
-LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, rmsnorm, geglu, selftest_shapes,
-config1 (default: all).
+LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, relpos_fp32, rmsnorm, geglu,
+selftest_shapes, config1 (default: all).
 
 A "step" is one forward + backward pass of a kernel over one batch of synthetic input that is
 already resident in HBM (3 and 5; config 4 is the forward-only attention
@@ -43,6 +43,7 @@ import torch  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, published
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, published
+PEAK_FP32_TFLOPS = 157.3       # MI355X fp32 MFMA, published
 METRIC = "HBM GB/s (RMSNorm/GEGLU) + TFLOP/s relpos attn fwd+bwd, 1 MI355X"
 CACHE_BYTES = (32 + 256) << 20  # L2 (8 XCDs x 4 MB) + MALL
 # The reference kernels' own fwd+bwd times at its selftest shapes on one H20-3e
@@ -151,8 +152,8 @@ def _kernel_line(ms: float, work: int, unit: str) -> dict:
     return {"ms": round(ms, 4), key: work, unit: round(_rate(work, ms, 1e9 if unit == "GB/s" else 1e12), 1)}
 
 
-def _roofline(value: float, unit: str) -> dict:
-    peak, bound = (PEAK_HBM_GBS, "hbm") if unit == "GB/s" else (PEAK_BF16_TFLOPS, "mfma")
+def _roofline(value: float, unit: str, peak_tflops: float = PEAK_BF16_TFLOPS) -> dict:
+    peak, bound = (PEAK_HBM_GBS, "hbm") if unit == "GB/s" else (peak_tflops, "mfma")
     return {"bound": bound, "achieved": round(value, 2), "peak": peak, "unit": unit,
             "frac": round(value / peak, 4), "traffic": None}
 
@@ -298,7 +299,8 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, dtype=torch.bfloat16) -> dict:
     import _hip
     scale = 1.0 / math.sqrt(D)
     nset, lag = 4, 2  # 4 x (qkv + dout) = 0.54 GB of inputs, plus per-set out32 and lse
-    dname = "bf16" if dtype == torch.bfloat16 else "fp16"
+    dname = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    peak = PEAK_FP32_TFLOPS if dtype == torch.float32 else PEAK_BF16_TFLOPS
     qkvs = [_gen((B * S, 3 * H * D), 0 if i == 0 else 100 + i, dtype=dtype) for i in range(nset)]
     douts = [_gen((B * S, H * D), 2 if i == 0 else 200 + i, dtype=dtype) for i in range(nset)]
     qkv_dev = [q.cuda() for q in qkvs]
@@ -321,9 +323,10 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, dtype=torch.bfloat16) -> dict:
     tb = _time_steps(_rotating(bwd, nset), args.steps, args.warmup, st)
     warm = _time_steps(lambda: (fwd(0), bwd(0)), args.steps, args.warmup, st)
     tfl = _rate(total, t["ms_mean"], 1e12)
-    suffix = ")" if dname == "bf16" else " shape, fp16 activations)"
+    cfg = "BASELINE config 5" if (B, S, H, D) == (4, 4096, 16, 64) else "BASELINE config 4 shape, fwd+bwd"
+    suffix = ")" if dname == "bf16" else f" shape, {dname} activations)" if "5" in cfg else f", {dname} activations)"
     res = {"workload": f"relpos attention fwd+bwd B{B} H{H} L{S} D{D} {dname}, pd fp32 [H,2L-1] "
-                       f"(BASELINE config 5{suffix}",
+                       f"({cfg}{suffix}",
            "value": round(tfl, 2), "unit": "TFLOP/s", "ms_per_step": round(t["ms_mean"], 4),
            "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_flops": total,
            "rotation": f"{nset} input sets (qkv, dout), backward lags forward by {lag}",
@@ -331,9 +334,9 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, dtype=torch.bfloat16) -> dict:
                        "relpos_bwd (dq+delta+dpd, dkdv, dpd reduce)": _kernel_line(tb["ms_mean"], fl_bwd, "TFLOP/s")},
            "mall_warm": {"ms_per_step": round(warm["ms_mean"], 4),
                          "TFLOP/s": round(_rate(total, warm["ms_mean"], 1e12), 1)},
-           "roofline": {**_roofline(tfl, "TFLOP/s"),
-                        "scope": "one fwd+bwd step = relpos_fwd_kernel + relpos_bwd_dq_kernel + "
-                                 "relpos_bwd_dkdv_kernel + relpos_dpd_reduce4, 14*B*H*L^2*D flops"}}
+           "roofline": {**_roofline(tfl, "TFLOP/s", peak),
+                        "scope": "one fwd+bwd step = forward + dQ + dK/dV + dpd reduce kernels, "
+                                 "14*B*H*L^2*D flops" + (" on fp32 MFMA" if dname == "fp32" else "")}}
     if not args.no_cpu and dname == "bf16":
         nb = 2  # bounded sample: 2 of the B*H = 64 (batch, head) pairs, full L
         q0, d0 = qkvs[0], douts[0]
@@ -509,7 +512,7 @@ def measured_copy_gbs() -> float:
     return round(2 * 2 * n / (ms * 1e-3) / 1e9, 1)
 
 
-ALL = "relpos,relpos_fwd,relpos_fp16,rmsnorm,geglu,selftest_shapes,config1"
+ALL = "relpos,relpos_fwd,relpos_fp16,relpos_fp32,rmsnorm,geglu,selftest_shapes,config1"
 
 
 def main() -> None:
@@ -537,6 +540,8 @@ def main() -> None:
         comps["relpos_attention_fwd_config4"] = bench_relpos_fwd_config4(args)
     if "relpos_fp16" in only:
         comps["relpos_attention_fp16"] = bench_relpos(args, dtype=torch.float16)
+    if "relpos_fp32" in only:
+        comps["relpos_attention_fp32"] = bench_relpos(args, B=2, S=1024, H=16, D=72, dtype=torch.float32)
     if "rmsnorm" in only:
         comps["rmsnorm"] = bench_rmsnorm(args)
     if "geglu" in only:

@@ -65,7 +65,7 @@ def test_geglu_graph_replay_matches_eager(approximate, dt):
     _replay_matches(lambda a: G.geglu(a, approximate=approximate), [u], gy, lambda: G.geglu(other))
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bfloat16", "float16"])
+@pytest.mark.parametrize("dt", DTYPES, ids=lambda d: str(d).replace("torch.", ""))
 def test_t5_table_chain_graph_replay_matches_eager(dt):
     B, S, H, D = 1, 256, 4, 64
     log(f"t5 table + relpos graph replay B{B} S{S} H{H} D{D} {dt}")

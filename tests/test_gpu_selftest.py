@@ -74,11 +74,14 @@ def test_rmsnorm_geglu_selftest_other_dtypes(dt):
                              lambda u: G.reference(u, approximate="tanh"), [u], time=False))
 
 
-def test_relpos_selftest_fp16():
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32], ids=["float16", "float32"])
+def test_relpos_selftest_other_dtypes(dt):
+    """fp16, and fp32 on fp32 MFMA: in fp32 the eager original equals the fp32 reference up to
+    summation order, so the criterion is its floors (rel-L2 1e-5, 1e-3 of the peak per element)."""
     B, S, H, D = 2, 256, 4, 64
-    log(f"selftest_autograd relpos fp16 B{B} S{S} H{H} D{D} + torch.compile(fullgraph)")
+    log(f"selftest_autograd relpos {dt} B{B} S{S} H{H} D{D} + torch.compile(fullgraph)")
     torch.manual_seed(0)
-    qkv = (0.6 * seeded((B * S, 3 * H * D), 0, dtype=torch.float32)).to(torch.float16)
+    qkv = (0.6 * seeded((B * S, 3 * H * D), 0, dtype=torch.float32)).to(dt)
     pd = seeded((H, 2 * S - 1), 1, dtype=torch.float32)
     _check(selftest_autograd(lambda q, p: A.relpos_attention(q, p, B, S, H, D, 1.0),
                              lambda q, p: A.reference(q, p, B, S, H, D, 1.0), [qkv, pd], time=False))
