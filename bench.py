@@ -8,7 +8,7 @@ timed on the host CPU beside it.
     python bench.py [--steps K] [--warmup W] [--only LIST] [--no-cpu] [--cpu-seconds S]
 
 LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, relpos_fp32, rmsnorm, geglu,
-selftest_shapes, config1 (default: all).
+geglu_linear, selftest_shapes, config1 (default: all).
 
 A "step" is one forward + backward pass of a kernel over one batch of synthetic input that is
 already resident in HBM (3 and 5; config 4 is the forward-only attention
@@ -367,6 +367,31 @@ def bench_relpos_fwd_config4(args) -> dict:
             "rotation": f"{nset} input sets", "roofline": _roofline(tfl, "TFLOP/s")}
 
 
+def bench_geglu_linear(args) -> dict:
+    """The merged gate|up projection feeding GEGLU at config 3's u [8192, 8192] (K = 4096): the
+    fused kernel (geglu_linear, u never written) against the unfused pair (hipBLASLt GEMM via
+    torch, then the GEGLU forward kernel). Forward only: the fused op exists for the forward."""
+    import _hip
+    rows, K, F = 8192, 4096, 4096
+    nset = 2
+    xs = [_gen((rows, K), 30 + i).cuda() for i in range(nset)]
+    ws = [(_gen((2 * F, K), 40 + i, dtype=torch.float32) / K ** 0.5).to(torch.bfloat16).cuda() for i in range(nset)]
+    st = torch.cuda.current_stream()
+    tf = _time_steps(_rotating(lambda i: _hip.geglu_linear_fwd(xs[i], ws[i], "tanh"), nset), args.steps, args.warmup, st)
+    tu = _time_steps(_rotating(lambda i: _hip.geglu_fwd(torch.nn.functional.linear(xs[i], ws[i]), "tanh"), nset),
+                     args.steps, args.warmup, st)
+    tg = _time_steps(_rotating(lambda i: torch.nn.functional.linear(xs[i], ws[i]), nset), args.steps, args.warmup, st)
+    fl = 2 * rows * 2 * F * K
+    tfl = _rate(fl, tf["ms_mean"], 1e12)
+    return {"workload": f"merged projection + GEGLU forward, x [{rows},{K}] bf16, w [{2 * F},{K}], gelu tanh",
+            "value": round(tfl, 1), "unit": "TFLOP/s", "ms_per_step": round(tf["ms_mean"], 4),
+            "algorithmic_flops": fl, "roofline": _roofline(tfl, "TFLOP/s"),
+            "unfused": {"ms": round(tu["ms_mean"], 4), "gemm_ms": round(tg["ms_mean"], 4),
+                        "gemm_TFLOP/s": round(_rate(fl, tg["ms_mean"], 1e12), 1),
+                        "note": "hipBLASLt GEMM (torch) writes u, then the GEGLU forward kernel reads it"},
+            "fused_vs_unfused": round(tu["ms_mean"] / tf["ms_mean"], 3)}
+
+
 def bench_selftest_shapes(args) -> dict:
     """The reference's selftest() shapes (its only published timings, on an H20-3e), timed as
     that selftest times them: one input set, forward + backward back to back. These working
@@ -512,7 +537,7 @@ def measured_copy_gbs() -> float:
     return round(2 * 2 * n / (ms * 1e-3) / 1e9, 1)
 
 
-ALL = "relpos,relpos_fwd,relpos_fp16,relpos_fp32,rmsnorm,geglu,selftest_shapes,config1"
+ALL = "relpos,relpos_fwd,relpos_fp16,relpos_fp32,rmsnorm,geglu,geglu_linear,selftest_shapes,config1"
 
 
 def main() -> None:
@@ -546,6 +571,8 @@ def main() -> None:
         comps["rmsnorm"] = bench_rmsnorm(args)
     if "geglu" in only:
         comps["geglu"] = bench_geglu(args, "none")
+    if "geglu_linear" in only:
+        comps["geglu_linear"] = bench_geglu_linear(args)
     if "selftest_shapes" in only:
         comps["selftest_shapes"] = bench_selftest_shapes(args)
     if "config1" in only:

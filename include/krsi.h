@@ -123,6 +123,16 @@ int krsi_geglu_bwd(const void* g, const void* u, void* du, int64_t rows, int32_t
 int krsi_geglu_bwd_bf16(const void* g, const void* u, void* du, int64_t rows, int32_t f,
                         int32_t approximate, void* stream);
 
+/* Merged gate|up projection with the GEGLU forward as its epilogue (the merged GEMM
+ * whose output library/geglu.py:3-5 takes as u), without writing u to memory:
+ *   u   = T(x w^T)      x: [rows, k], w: [2f, k] = [W_gate; W_up] (nn.Linear layout)
+ *   out = T( T(gelu(u[:, :f])) * u[:, f:] )                        out: [rows, f]
+ * with the rounding points of krsi_geglu_fwd applied to the GEMM output rounded to T.
+ * dtype: KRSI_DTYPE_BF16 or KRSI_DTYPE_F16 (T). Limits: k % 64 == 0, f % 64 == 0,
+ * 128 * k * 2 < 2^31; x and w 16-byte aligned, contiguous. */
+int krsi_geglu_linear_fwd(const void* x, const void* w, void* out, int64_t rows, int32_t k,
+                          int32_t f, int32_t approximate, int32_t dtype, void* stream);
+
 /* ------------------------------------------------- relative-position attention
  * Replaces library/relpos_attention.py:132-140 (_forward: _fwd :26-59).
  * dtype (T): KRSI_DTYPE_BF16 or KRSI_DTYPE_F16 run on 16-bit MFMA, and P is rounded

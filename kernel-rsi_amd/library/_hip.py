@@ -32,6 +32,7 @@ SIGNATURES = {
     "krsi_geglu_fwd_bf16": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P]),
     "krsi_geglu_bwd": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _I32, _P]),
     "krsi_geglu_bwd_bf16": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _P]),
+    "krsi_geglu_linear_fwd": (ctypes.c_int, [_P, _P, _P, _I64, _I32, _I32, _I32, _I32, _P]),
     "krsi_relpos_fwd": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _I32, _P]),
     "krsi_relpos_fwd_bf16": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _P]),
     "krsi_relpos_bwd_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
@@ -186,6 +187,26 @@ def geglu_bwd(g: torch.Tensor, u: torch.Tensor, approximate: str = "tanh") -> to
         _check(lib().krsi_geglu_bwd(_ptr(g), _ptr(u), _ptr(du), rows, f2 // 2,
                                     _approx(approximate), dt, _stream(u)))
     return du
+
+
+def geglu_linear_fwd(x: torch.Tensor, w: torch.Tensor, approximate: str = "tanh") -> torch.Tensor:
+    """gelu(x @ w[:F].T) * (x @ w[F:].T) for x [rows, K] and the merged weight w [2F, K] in one
+    kernel (bf16 or fp16; K and F multiples of 64)."""
+    _on_gpu(x, w)
+    dt = _dtype("x", x, allowed=(torch.bfloat16, torch.float16))
+    _dtype("weight", w, like=x)
+    if x.dim() != 2 or w.dim() != 2 or w.shape[1] != x.shape[1] or w.shape[0] % 2:
+        raise ValueError(f"need x [rows, K] and w [2F, K], got {tuple(x.shape)} and {tuple(w.shape)}")
+    rows, k = x.shape
+    f = w.shape[0] // 2
+    if k % 64 or f % 64:
+        raise ValueError(f"geglu_linear needs K and F multiples of 64, got K={k}, F={f}")
+    x, w = x.contiguous(), w.contiguous()
+    out = torch.empty(rows, f, device=x.device, dtype=x.dtype)
+    if rows:
+        _check(lib().krsi_geglu_linear_fwd(_ptr(x), _ptr(w), _ptr(out), rows, k, f, _approx(approximate), dt,
+                                           _stream(x)))
+    return out
 
 
 # ------------------------------------------------ relative-position attention

@@ -6,8 +6,8 @@ replay.py's per-file module names) does not register the ops twice.
 
 Op names follow the reference (library/rmsnorm.py:86-103, geglu.py:85-101,
 relpos_attention.py:175-195): krsi::rmsnorm_fwd/bwd, krsi::geglu_fwd/bwd,
-krsi::relpos_attn_fwd/bwd; krsi::relpos_bucket_gather/sum (the T5 table step) have
-no counterpart there. Their schemas are internal to this library.
+krsi::relpos_attn_fwd/bwd; krsi::relpos_bucket_gather/sum (the T5 table step) and
+krsi::geglu_linear_fwd (the merged projection with the GEGLU epilogue) have no counterpart there. Their schemas are internal to this library.
 """
 from __future__ import annotations
 
@@ -85,6 +85,31 @@ def _geglu_backward(ctx, g):
 
 
 geglu_fwd_op.register_autograd(_geglu_backward, setup_context=_geglu_setup)
+
+
+@torch.library.custom_op("krsi::geglu_linear_fwd", mutates_args=())
+def geglu_linear_fwd_op(x: Tensor, w: Tensor, approximate: str) -> Tensor:
+    return _hip.geglu_linear_fwd(x, w, approximate)
+
+
+@geglu_linear_fwd_op.register_fake
+def _(x, w, approximate):
+    return x.new_empty((x.shape[0], w.shape[0] // 2))
+
+
+def _geglu_linear_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0], inputs[1])
+    ctx.approximate = inputs[2]
+
+
+def _geglu_linear_backward(ctx, g):
+    x, w = ctx.saved_tensors
+    u = torch.nn.functional.linear(x, w)  # recomputed: the forward never wrote it
+    du = geglu_bwd_op(g.contiguous(), u, ctx.approximate)
+    return du @ w, du.t().contiguous() @ x, None
+
+
+geglu_linear_fwd_op.register_autograd(_geglu_linear_backward, setup_context=_geglu_linear_setup)
 
 # ------------------------------------------------ relative-position attention
 

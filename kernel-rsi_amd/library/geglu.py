@@ -44,9 +44,42 @@ def geglu(u, *, approximate="tanh"):
     return GEGLU.apply(u, approximate)
 
 
+class GEGLULinear(torch.autograd.Function):
+    """Eager path of geglu_linear: one fused kernel forward; the backward recomputes u with the
+    vendor GEMM (the forward never wrote it), runs the GEGLU backward kernel on it, and forms
+    dx = du w and dw = du^T x with the vendor GEMM."""
+
+    @staticmethod
+    def forward(ctx, x, w, approximate):
+        ctx.save_for_backward(x, w)
+        ctx.approximate = approximate
+        return _hip.geglu_linear_fwd(x, w, approximate)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        u = torch.nn.functional.linear(x, w)
+        du = _hip.geglu_bwd(g.contiguous(), u, ctx.approximate)
+        return du @ w, du.t().contiguous() @ x, None
+
+
+def geglu_linear(x, w, *, approximate="tanh"):
+    """geglu(x @ w.T) for x [rows, K] and the merged weight w = cat([W_gate, W_up]) [2F, K], with
+    the GEGLU forward fused into the projection's epilogue (u is never written). bf16 or fp16;
+    K and F multiples of 64. Differentiable in x and w."""
+    if compiling():
+        return _ops().geglu_linear_fwd_op(x, w, approximate)
+    return GEGLULinear.apply(x, w, approximate)
+
+
 def reference(u, *, approximate="tanh"):
     a, b = u.chunk(2, dim=-1)
     return torch.nn.functional.gelu(a, approximate=approximate) * b
+
+
+def reference_linear(x, w, *, approximate="tanh"):
+    """The unfused pair geglu_linear stands for: the merged projection, then reference()."""
+    return reference(torch.nn.functional.linear(x, w), approximate=approximate)
 
 
 def selftest():

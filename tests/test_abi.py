@@ -120,6 +120,20 @@ def test_noalloc_backward_validates_before_touching_the_device():
     assert "16 MiB" in lib.krsi_error_string(TOO_LARGE).decode()
 
 
+def test_geglu_linear_validates_before_launch():
+    lib = _hip.lib()
+    f = lib.krsi_geglu_linear_fwd
+    assert f(FAKE, FAKE, FAKE, 4, 64, 64, 1, 2, NULL) == 5        # fp32: not built
+    assert f(FAKE, FAKE, FAKE, 4, 64, 64, 2, 0, NULL) == 5        # unknown GELU form
+    assert f(FAKE, FAKE, FAKE, 4, 96, 64, 1, 0, NULL) == 5        # K % 64 != 0
+    assert f(FAKE, FAKE, FAKE, 4, 64, 96, 1, 0, NULL) == 5        # F % 64 != 0
+    assert f(FAKE, FAKE, FAKE, 4, 1 << 23, 64, 1, 0, NULL) == 5   # a stage's offsets past 2^31
+    assert f(FAKE, FAKE, FAKE, -1, 64, 64, 1, 0, NULL) == 2
+    assert f(NULL, FAKE, FAKE, 4, 64, 64, 1, 0, NULL) == 1
+    assert f(FAKE + 2, FAKE, FAKE, 4, 64, 64, 1, 0, NULL) == 3
+    assert f(NULL, NULL, NULL, 0, 64, 64, 1, 0, NULL) == 0         # no rows: no-op
+
+
 def test_dtype_argument_validated_before_launch():
     """The generic entry points take KRSI_DTYPE_* (0 bf16, 1 fp16, 2 fp32); an unknown code,
     or fp32 for attention, is UNSUPPORTED before anything is launched (FAKE pointers)."""
