@@ -29,6 +29,7 @@ namespace {
 constexpr int kGlRows = 128;   // rows (of x and out) per workgroup
 constexpr int kGlCols = 64;    // output columns per workgroup: 128 rows of w (64 gate + 64 up)
 constexpr int kGlK = 64;       // K per stage
+constexpr int kGlGroup = 4;    // row blocks per tile group (tile order, below)
 constexpr int kGlThreads = 256;
 constexpr int kGlTile = 128 * kGlK;  // 16-bit elements per staged tile (x or w)
 constexpr int kGlChunks = kGlTile / 8;
@@ -60,15 +61,24 @@ __device__ __forceinline__ int toff(int r, int j) { return r * kGlK + 8 * (j ^ s
 template <int DT, bool TANH>
 __global__ __launch_bounds__(kGlThreads, 2) void geglu_linear_fwd_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
-    int64_t rows, int K, int F, int ncb) {
+    int64_t rows, int K, int F, int ncb, int nrb) {
   __shared__ __attribute__((aligned(16))) uint16_t Xs[2 * kGlTile];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2 * kGlTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int wr = wave >> 1, wc = wave & 1;
-  // XCD-aware order: consecutive tiles of one XCD share their x rows (same row block).
+  // Tile order. xcd_tile gives each XCD a contiguous range of tiles. Inside it the tiles go in
+  // groups of kGlGroup row blocks: consecutive tiles walk the group's row blocks first, then
+  // its column blocks. The workgroups in flight on one XCD then share a few row blocks of x
+  // and a few column blocks of w in that XCD's L2. Walking one row block across every column
+  // block instead made each XCD stream all of w once per row block it owns: 4.4 GB fetched per
+  // call at x [8192, 4096], F = 4096, against 0.13 GB of inputs.
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int64_t m0 = (int64_t)(tile / ncb) * kGlRows;
-  const int c0 = (tile % ncb) * kGlCols;
+  const int per_group = kGlGroup * ncb;
+  const int grp = tile / per_group, in_grp = tile - grp * per_group;
+  const int rb0 = grp * kGlGroup;
+  const int gsz = min(kGlGroup, nrb - rb0);
+  const int64_t m0 = (int64_t)(rb0 + in_grp % gsz) * kGlRows;
+  const int c0 = (in_grp / gsz) * kGlCols;
 
   // DMA: thread chunk p = k * 256 + tid of a tile is staged row p / 8, position p % 8, which
   // holds logical chunk (p % 8) ^ swz(row). Rows 0-63 of the w tile are gate rows c0 .., rows
@@ -164,15 +174,16 @@ template <int DT>
 int launch_geglu_linear(const void* x, const void* w, void* out, int64_t rows, int K, int F, bool tanh_form,
                         hipStream_t st) {
   const int ncb = F / kGlCols;
-  const int64_t tiles = ceil_div(rows, kGlRows) * ncb;
+  const int64_t nrb = ceil_div(rows, kGlRows);
+  const int64_t tiles = nrb * ncb;
   if (tiles > 0x7fffffff) return KRSI_ERR_BAD_SHAPE;
   const dim3 grid((unsigned)tiles);
   if (tanh_form)
     hipLaunchKernelGGL((geglu_linear_fwd_kernel<DT, true>), grid, dim3(kGlThreads), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)w, (uint16_t*)out, rows, K, F, ncb);
+                       (const uint16_t*)w, (uint16_t*)out, rows, K, F, ncb, (int)nrb);
   else
     hipLaunchKernelGGL((geglu_linear_fwd_kernel<DT, false>), grid, dim3(kGlThreads), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)w, (uint16_t*)out, rows, K, F, ncb);
+                       (const uint16_t*)w, (uint16_t*)out, rows, K, F, ncb, (int)nrb);
   return launch_status();
 }
 
