@@ -45,8 +45,8 @@
 //   * Online softmax keeps the exact running max per 64-key step (the step
 //     maximum gives p = 1, exact in bf16, as in the reference); the fp32
 //     accumulators are rescaled only when some lane's max moved. The row sum
-//     adds the fp32 p (fp16) or the bf16 p the PV product uses (bf16:
-//     v_dot2c_f32_bf16, two per op).
+//     adds the fp32 p, as the reference; the PV product takes p rounded to the
+//     activation dtype.
 //   * dpd is reduced along the diagonals j - i inside the dK/dV kernel: each
 //     (wave, half-wave) adds its fp32 ds into private LDS rings indexed by
 //     diagonal, two diagonals per 64-bit read-modify-write. Within one
@@ -356,24 +356,11 @@ __device__ __forceinline__ f32x16 read_bias16(const float* bw, int x0) {
   return out;
 }
 
-// The forward's row sum l: of the fp32 p, as the reference (relpos_attention.py:51), or of
-// the rounded p the P V product uses, two per v_dot2c_f32_bf16 / _f16 against (1, 1).
-template <int DT>
-constexpr bool kRowSumFp32 = (DT == kF16);
-template <int DT>
-__device__ __forceinline__ float add_pair(uint32_t pair, float acc) {
-  if constexpr (DT == kF16)
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), __builtin_bit_cast(f16x2, 0x3c003c00u),
-                                  acc, false);
-  else
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
-                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
-}
-
 // ------------------------------------------------------------------- forward
 // One 64-key step of the forward for this lane's query: scores (bias folded into
-// the accumulator), exact running max, p = exp2(acc c - m), l += bf16(p),
-// O^T += V^T P^T. TAIL masks keys >= S (last step only).
+// the accumulator), exact running max, p = exp2(acc c - m), l += p (fp32, as the
+// reference's row sum, relpos_attention.py:51), O^T += V^T P^T with P rounded to the
+// activation dtype. TAIL masks keys >= S (last step only).
 template <int DT, int DP, int NW, bool TAIL>
 __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs, const float* Bw,
                                          const TileLane<DP>& L, const u32x4* qreg, f32x16* oacc,
@@ -425,13 +412,8 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const u32x4 pb = Elem<DT>::pack(&p[8 * u]);
-      if constexpr (kRowSumFp32<DT>) {
 #pragma unroll
-        for (int w = 0; w < 8; ++w) l_run[w & 1] += p[8 * u + w];
-      } else {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) l_run[w & 1] = add_pair<DT>(pb[w], l_run[w & 1]);
-      }
+      for (int w = 0; w < 8; ++w) l_run[w & 1] += p[8 * u + w];
 #pragma unroll
       for (int db = 0; db < G::DB; ++db)
         oacc[db] = mfma32x32x16<DT>(tr_operand<DP>(Vs, L, 2 * kb + u, db), pb, oacc[db]);
