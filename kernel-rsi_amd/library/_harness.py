@@ -205,9 +205,13 @@ class Timer:
         return [start.elapsed_time(stop) / len(self.fns) for start, stop in marks]
 
     def host_sync(self) -> str | None:
-        """The first host synchronisation the callables make (None if they make none). Found
-        with torch's sync debug mode, before any capture is attempted: a capture that fails
-        part-way leaves the process's graph state unusable."""
+        """The first host synchronisation the callables make once warm (None if they make
+        none). Found with torch's sync debug mode on the second call: the first, unprobed,
+        leaves one-time work out (a torch.compile compilation synchronises), and it comes
+        before any capture is attempted, since a capture that fails part-way leaves the
+        process's graph state unusable."""
+        self.fns[0]()
+        torch.cuda.synchronize()
         before = torch.cuda.get_sync_debug_mode()
         torch.cuda.set_sync_debug_mode("error")
         try:

@@ -26,3 +26,13 @@ def test_time_ab_uses_one_mode_for_all_variants():
     res = time_ab({"graphable": [lambda: x * 2], "syncs": [lambda: (x * 2).sum().item()]}, rounds=2, reps=3)
     assert res["graphable"]["mode"] == res["syncs"]["mode"] == "eager"
     assert "could not be graph-captured" in res["graphable"]["note"] and "host sync" in res["graphable"]["note"]
+
+
+def test_compiled_callable_is_timed_by_graph_replay():
+    # A torch.compile'd callable synchronises while it compiles, on its first call only; the
+    # harness probes for host syncs after one warm call, so the compiled callable is captured.
+    log("harness: compiled callable timed by graph replay")
+    x = torch.randn(1 << 16, device="cuda")
+    f = torch.compile(lambda: x * 2 + 1)
+    res = time_calls([f], reps=2)
+    assert res["mode"] == "graph", res.get("note")
