@@ -1,6 +1,7 @@
-"""RMSNorm, GEGLU and the T5 table step captured in HIP graphs: every entry point of the
-library allocates, frees and synchronizes nothing, so a captured fwd+bwd replays to the eager
-result. Replayed three times with unrelated eager work in between, each replay checked."""
+"""RMSNorm, GEGLU, the fused projection and the T5 table step captured in HIP graphs: every
+entry point of the library allocates, frees and synchronizes nothing, so a captured fwd+bwd
+replays to the eager result. Replayed three times with unrelated eager work in between, each
+replay checked."""
 import pytest
 import torch
 
@@ -75,3 +76,16 @@ def test_t5_table_chain_graph_replay_matches_eager(dt):
     A.t5_relative_position_bucket(S, True, 32, 128, "cuda")  # build the cached map before capture
     _replay_matches(lambda q, t: A.relpos_attention(q, A.t5_relpos_table(t, S), B, S, H, D, 0.125),
                     [qkv, table], dout, lambda: A.t5_relpos_table(table, 64))
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=lambda d: str(d).replace("torch.", ""))
+def test_geglu_linear_graph_replay_matches_eager(dt):
+    # The fused projection's forward kernel and its backward (vendor GEMMs around the GEGLU
+    # backward kernel), captured and replayed.
+    rows, K, F = 256, 512, 256
+    log(f"geglu_linear graph replay x [{rows}, {K}] w [{2 * F}, {K}] {dt}")
+    x = seeded((rows, K), 10, dtype=dt)
+    w = (seeded((2 * F, K), 11, dtype=torch.float32) / K ** 0.5).to(dt)
+    gy = seeded((rows, F), 12, dtype=dt)
+    other = seeded((64, 256), 13)
+    _replay_matches(lambda a, b: G.geglu_linear(a, b, approximate="tanh"), [x, w], gy, lambda: G.geglu(other))
