@@ -106,7 +106,9 @@ def _geglu_linear_backward(ctx, g):
     x, w = ctx.saved_tensors
     u = torch.nn.functional.linear(x, w)  # recomputed: the forward never wrote it
     du = geglu_bwd_op(g.contiguous(), u, ctx.approximate)
-    return du @ w, du.t().contiguous() @ x, None
+    dx = du @ w if ctx.needs_input_grad[0] else None
+    dw = du.t().contiguous() @ x if ctx.needs_input_grad[1] else None
+    return dx, dw, None
 
 
 geglu_linear_fwd_op.register_autograd(_geglu_linear_backward, setup_context=_geglu_linear_setup)

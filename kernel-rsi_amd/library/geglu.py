@@ -60,7 +60,9 @@ class GEGLULinear(torch.autograd.Function):
         x, w = ctx.saved_tensors
         u = torch.nn.functional.linear(x, w)
         du = _hip.geglu_bwd(g.contiguous(), u, ctx.approximate)
-        return du @ w, du.t().contiguous() @ x, None
+        dx = du @ w if ctx.needs_input_grad[0] else None
+        dw = du.t().contiguous() @ x if ctx.needs_input_grad[1] else None
+        return dx, dw, None
 
 
 def geglu_linear(x, w, *, approximate="tanh"):

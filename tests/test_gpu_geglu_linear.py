@@ -46,3 +46,24 @@ def test_geglu_linear_is_the_gemm_output_rounded_then_geglu():
     unfused = G.geglu(torch.nn.functional.linear(x, w))
     rel = ((fused.float() - unfused.float()).abs() / (unfused.float().abs() + 1e-2)).max().item()
     assert rel < 0.05, rel
+
+
+@pytest.mark.parametrize("compiled", [False, True], ids=["eager", "compiled"])
+def test_geglu_linear_frozen_weight_gets_no_gradient(compiled):
+    """With the weight frozen the backward forms only dx, which equals the dx of the full
+    backward bitwise (the same kernels on the same inputs)."""
+    rows, K, F = 256, 512, 128
+    log(f"geglu_linear frozen weight, {'compiled' if compiled else 'eager'}")
+    x0 = seeded((rows, K), 5)
+    w0 = (seeded((2 * F, K), 6, dtype=torch.float32) / K ** 0.5).to(torch.bfloat16)
+    gy = seeded((rows, F), 7)
+    fn = lambda a, b: G.geglu_linear(a, b)  # noqa: E731
+    if compiled:
+        torch._dynamo.reset()
+        fn = torch.compile(fn, fullgraph=True)
+    x, w = x0.clone().requires_grad_(True), w0.clone()
+    fn(x, w).backward(gy)
+    assert w.grad is None
+    xf, wf = x0.clone().requires_grad_(True), w0.clone().requires_grad_(True)
+    fn(xf, wf).backward(gy)
+    assert torch.equal(x.grad, xf.grad) and wf.grad is not None
