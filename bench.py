@@ -329,6 +329,7 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, dtype=torch.bfloat16) -> dict:
                        f"({cfg}{suffix}",
            "value": round(tfl, 2), "unit": "TFLOP/s", "ms_per_step": round(t["ms_mean"], 4),
            "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_flops": total,
+           "matrix_dtype": dname,
            "rotation": f"{nset} input sets (qkv, dout), backward lags forward by {lag}",
            "kernels": {"relpos_fwd": _kernel_line(tf["ms_mean"], fl_fwd, "TFLOP/s"),
                        "relpos_bwd (dq+delta+dpd, dkdv, dpd reduce)": _kernel_line(tb["ms_mean"], fl_bwd, "TFLOP/s")},
@@ -364,7 +365,7 @@ def bench_relpos_fwd_config4(args) -> dict:
     return {"workload": f"relpos attention fwd B{B} H{H} L{S} D{D} bf16 (BASELINE config 4)",
             "value": round(tfl, 1), "unit": "TFLOP/s", "ms_per_step": round(t["ms_mean"], 4),
             "host_enqueue_ms_per_step": round(t["host_ms"], 4), "algorithmic_flops": fl,
-            "rotation": f"{nset} input sets", "roofline": _roofline(tfl, "TFLOP/s")}
+            "matrix_dtype": "bf16", "rotation": f"{nset} input sets", "roofline": _roofline(tfl, "TFLOP/s")}
 
 
 def bench_geglu_linear(args) -> dict:
@@ -385,6 +386,7 @@ def bench_geglu_linear(args) -> dict:
     tfl = _rate(fl, tf["ms_mean"], 1e12)
     return {"workload": f"merged projection + GEGLU forward, x [{rows},{K}] bf16, w [{2 * F},{K}], gelu tanh",
             "value": round(tfl, 1), "unit": "TFLOP/s", "ms_per_step": round(tf["ms_mean"], 4),
+            "matrix_dtype": "bf16",
             "algorithmic_flops": fl, "roofline": _roofline(tfl, "TFLOP/s"),
             "unfused": {"ms": round(tu["ms_mean"], 4), "gemm_ms": round(tg["ms_mean"], 4),
                         "gemm_TFLOP/s": round(_rate(fl, tg["ms_mean"], 1e12), 1),
@@ -487,6 +489,23 @@ def attach_stream_ceiling(comps: dict) -> dict:
     return {f"stream_r{r}w{w}_GB/s": v for (r, w), v in gbs.items()}
 
 
+def attach_gemm_ceiling(comps: dict) -> dict:
+    """The vendor library's dense GEMM rate on this box (hw.py's probe: hipBLASLt through
+    torch.mm at 8192^3, per dtype), beside the published MFMA peak. It runs under the same
+    clock and power limits as the attention kernels, so each matrix component also gets its
+    fraction of it."""
+    import hw
+    if not any(c.get("matrix_dtype") for c in comps.values()):
+        return {}
+    rates = hw.probe_gemm(hw.Clock(samples=3), 8192)
+    for comp in comps.values():
+        rate = rates.get(comp.get("matrix_dtype"))
+        if rate:
+            comp["gemm_ceiling"] = {"TFLOP/s": rate, "frac": round(comp["value"] / rate, 4),
+                                    "source": f"hipBLASLt {comp['matrix_dtype']} GEMM 8192^3 (torch.mm), this run"}
+    return {f"gemm_{k}_TFLOP/s": v for k, v in rates.items() if isinstance(v, (int, float))}
+
+
 # ------------------------------------------------------------------- traffic
 def _csrc_sha256() -> str:
     import hashlib
@@ -578,7 +597,7 @@ def main() -> None:
     if "config1" in only:
         comps["rmsnorm_config1"] = bench_config1(args)
     attach_traffic(comps)
-    ceilings = attach_stream_ceiling(comps)
+    ceilings = {**attach_stream_ceiling(comps), **attach_gemm_ceiling(comps)}
     head = comps.get("relpos_attention") or next(c for c in comps.values() if "value" in c)
     cpu = cpu_model()
     line = {
