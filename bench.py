@@ -598,7 +598,12 @@ def main() -> None:
         comps["rmsnorm_config1"] = bench_config1(args)
     attach_traffic(comps)
     ceilings = {**attach_stream_ceiling(comps), **attach_gemm_ceiling(comps)}
-    head = comps.get("relpos_attention") or next(c for c in comps.values() if "value" in c)
+    # The headline is config 5's attention; a run limited by --only to components without a
+    # single figure of their own (the selftest shapes, config 1) prints value null.
+    head = comps.get("relpos_attention") or next((c for c in comps.values() if "value" in c), None)
+    if head is None:
+        head = {"value": None, "unit": None, "ms_per_step": None, "roofline": None,
+                "workload": "no headline component in --only " + args.only}
     cpu = cpu_model()
     line = {
         "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
