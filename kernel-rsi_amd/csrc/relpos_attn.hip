@@ -214,12 +214,14 @@ __device__ __forceinline__ u32x4 row_operand(const uint16_t* tile, const TileLan
 }
 
 // Lane l gets max / sum of x over lanes l % 32 and l % 32 + 32 (v_permlane32_swap_b32
-// exchanges the upper half of its first operand with the lower half of its second; the
-// nops cover the VALU-write -> permlane-read hazard).
+// exchanges the upper half of its first operand with the lower half of its second). The
+// builtin, unlike inline asm, leaves the scheduler free to move LDS accesses across it, and
+// the compiler inserts the VALU-write -> permlane-read wait itself.
 __device__ __forceinline__ void xhalf_pair(float x, float& a, float& b) {
-  a = x;
-  b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  a = __builtin_bit_cast(float, (unsigned)r[0]);
+  b = __builtin_bit_cast(float, (unsigned)r[1]);
 }
 __device__ __forceinline__ float xhalf_max(float x) {
   float a, b;
