@@ -89,3 +89,21 @@ def test_geglu_linear_graph_replay_matches_eager(dt):
     gy = seeded((rows, F), 12, dtype=dt)
     other = seeded((64, 256), 13)
     _replay_matches(lambda a, b: G.geglu_linear(a, b, approximate="tanh"), [x, w], gy, lambda: G.geglu(other))
+
+
+def test_launches_go_to_torch_current_stream():
+    # The binding reads torch's current stream per call (raw handle), so work queued on a side
+    # stream runs there, ordered after that stream's earlier work.
+    import _hip
+    log("current-stream handle on the default and a side stream")
+    x = seeded((64, 256), 0)
+    w = torch.ones(256, device="cuda", dtype=torch.bfloat16)
+    assert _hip._stream(x) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert _hip._stream(x) == side.cuda_stream
+        y, _ = _hip.rmsnorm_fwd(x, w, 1e-6)
+    torch.cuda.current_stream().wait_stream(side)
+    ref, _ = _hip.rmsnorm_fwd(x, w, 1e-6)
+    assert torch.equal(y, ref)
