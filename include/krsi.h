@@ -92,8 +92,8 @@ int krsi_rmsnorm_bwd_bf16(const void* g, const void* x, const void* w, const flo
  *   - the copy used is the current device's (the stream must belong to it);
  *   - its address is looked up once per device on the first call.
  * Limit: krsi_rmsnorm_bwd_workspace_bytes(rows, n) <= 16 MiB. That holds for
- * every row count when n <= 7936, and for fewer rows above that (n = 8192:
- * rows <= 496). Larger problems return KRSI_ERR_TOO_LARGE before anything is
+ * every row count when n <= 8192, and for fewer rows above that (n = 16384:
+ * rows <= 256). Larger problems return KRSI_ERR_TOO_LARGE before anything is
  * launched.
  * Allocates nothing: no hipMalloc, hipFree or allocating library call.
  * Calls that overlap on one GPU (several streams or host threads) share the

@@ -19,8 +19,8 @@
 // and the row lives in registers between the reduction and the write. The
 // backward is persistent: a fixed grid of NB workgroups walks the rows, keeps
 // its share of dw in fp32 registers and writes one partial row per workgroup;
-// two small column-sum passes reduce the partials in a fixed order, so dw is
-// bitwise reproducible. Rows whose length is not a multiple of 8, or whose
+// one small column-sum launch reduces the (at most 512) partials in a fixed
+// order, so dw is bitwise reproducible. Rows whose length is not a multiple of 8, or whose
 // pointers are not 16-byte aligned, take a scalar path with the same math.
 #include "krsi_device.h"
 #include "krsi_internal.h"
@@ -34,7 +34,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kBwdMaxBlocks = 512;     // persistent grid of the backward
-constexpr int kColsumRows = 32;        // partial rows folded per first-level column-sum block
+constexpr int kColsumWaves = 16;       // waves per column-sum workgroup (64 columns each)
 constexpr int kScalarRowChunk = 64;    // rows per block of the scalar dw kernel
 
 // ----------------------------------------------------------------- forward
@@ -314,34 +314,29 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_dw_scalar(const typename Ele
   part[(int64_t)blockIdx.y * n + col] = acc;
 }
 
-// Column sums of a [R, n] fp32 matrix in fixed order. Block (64 columns, row
-// group of `rpg` rows): lane = column, the 4 waves take every 4th row of the
-// group, then the 4 wave sums are added in wave order. FINAL writes dtype DT,
-// else one fp32 row per row group for the next level. Many small blocks keep
-// enough loads in flight to stream the partials at HBM rate.
-template <bool FINAL, int DT = kBf16>
-__global__ __launch_bounds__(kThreads) void colsum(const float* __restrict__ in, int64_t R, int n,
-                                                   int64_t rpg, float* __restrict__ outf,
-                                                   typename Elem<DT>::T* __restrict__ outb) {
-  __shared__ float s[kWavesPerBlock][kWave];
+// dw = column sums of the [R, n] fp32 partial rows (R <= 512), in fixed order, in one launch.
+// Block = 64 columns (lane = column) and 16 waves: wave w adds rows w, w + 16, ... in order,
+// then wave 0 adds the 16 wave sums in wave order and writes dtype DT. Each wave has at most
+// 32 rows, all of whose loads it can have in flight.
+template <int DT>
+__global__ __launch_bounds__(kColsumWaves * kWave) void colsum(const float* __restrict__ in, int64_t R,
+                                                               int n, typename Elem<DT>::T* __restrict__ out) {
+  __shared__ float s[kColsumWaves][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int col = blockIdx.x * kWave + lane;
-  const int64_t r0 = (int64_t)blockIdx.y * rpg;
-  const int64_t r1 = r0 + rpg < R ? r0 + rpg : R;
   float acc = 0.f;
   if (col < n) {
-#pragma unroll 4
-    for (int64_t r = r0 + wave; r < r1; r += kWavesPerBlock) acc += in[r * n + col];
+#pragma unroll 8
+    for (int64_t r = wave; r < R; r += kColsumWaves) acc += in[r * n + col];
   }
   s[wave][lane] = acc;
   __syncthreads();
   if (wave == 0 && col < n) {
-    const float t = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
-    if (FINAL)
-      outb[col] = Elem<DT>::store(t);
-    else
-      outf[(int64_t)blockIdx.y * n + col] = t;
+    float t = s[0][lane];
+#pragma unroll
+    for (int w = 1; w < kColsumWaves; ++w) t += s[w][lane];
+    out[col] = Elem<DT>::store(t);
   }
 }
 
@@ -477,15 +472,8 @@ int rmsnorm_bwd(const void* g, const void* x, const void* w, const float* rstd, 
   }
   int rc = launch_status();
   if (rc != KRSI_OK) return rc;
-  float* part2 = reinterpret_cast<float*>(
-      static_cast<char*>(workspace) +
-      align256((size_t)bwd_partial_rows_max(rows, n) * n * sizeof(float)));
-  const int64_t p2 = ceil_div(p1, kColsumRows);
-  const unsigned ctiles = (unsigned)ceil_div(n, kWave);
-  hipLaunchKernelGGL((colsum<false, DT>), dim3(ctiles, (unsigned)p2), dim3(kThreads), 0, st,
-                     (const float*)part, p1, (int)n, (int64_t)kColsumRows, part2, (T*)nullptr);
-  hipLaunchKernelGGL((colsum<true, DT>), dim3(ctiles, 1), dim3(kThreads), 0, st, (const float*)part2,
-                     p2, (int)n, p2, (float*)nullptr, (T*)dw);
+  hipLaunchKernelGGL((colsum<DT>), dim3((unsigned)ceil_div(n, kWave)), dim3(kColsumWaves * kWave), 0, st,
+                     (const float*)part, p1, (int)n, (T*)dw);
   return launch_status();
 }
 
@@ -493,9 +481,8 @@ int rmsnorm_bwd(const void* g, const void* x, const void* w, const float* rstd, 
 template <int DT>
 int rmsnorm_bwd_empty(void* dw, int n, hipStream_t st) {
   using T = typename Elem<DT>::T;
-  hipLaunchKernelGGL((colsum<true, DT>), dim3((unsigned)ceil_div(n, kWave), 1), dim3(kThreads), 0,
-                     st, (const float*)nullptr, (int64_t)0, (int)n, (int64_t)1, (float*)nullptr,
-                     (T*)dw);
+  hipLaunchKernelGGL((colsum<DT>), dim3((unsigned)ceil_div(n, kWave)), dim3(kColsumWaves * kWave), 0, st,
+                     (const float*)nullptr, (int64_t)0, (int)n, (T*)dw);
   return launch_status();
 }
 
@@ -537,9 +524,7 @@ extern "C" {
 size_t krsi_rmsnorm_bwd_workspace_bytes(int64_t rows, int32_t n) {
   using namespace krsi;
   if (rows <= 0 || n <= 0) return 0;
-  const int64_t p1 = bwd_partial_rows_max(rows, n);
-  const int64_t p2 = ceil_div(p1, kColsumRows);
-  return align256((size_t)p1 * n * sizeof(float)) + align256((size_t)p2 * n * sizeof(float));
+  return align256((size_t)bwd_partial_rows_max(rows, n) * n * sizeof(float));
 }
 
 int krsi_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows, int32_t n,

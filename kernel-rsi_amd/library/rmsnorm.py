@@ -4,8 +4,8 @@ Each row is scaled by the reciprocal root of its mean square (fp32 arithmetic). 
 row is rounded to the input dtype before it is multiplied by the weight, as the reference
 formula below (and the eager models it stands in for) does. The forward keeps one fp32
 reciprocal root per row for the backward. The backward writes dx in a single pass over the rows.
-The weight gradient is summed into per-workgroup fp32 partial rows, which two small launches
-then add in a fixed order, so dw is bitwise reproducible. Row lengths up to 16384.
+The weight gradient is summed into per-workgroup fp32 partial rows, which one small launch
+then adds in a fixed order, so dw is bitwise reproducible. Row lengths up to 16384.
 Same public functions and arguments as the reference's library/rmsnorm.py:106-123; usable under
 torch.compile(fullgraph=True).
 """

@@ -110,12 +110,12 @@ def test_noalloc_backward_validates_before_touching_the_device():
     assert f(FAKE, FAKE, FAKE, FAKE, FAKE, NULL, 4, 64, 0, NULL) == 1         # dw NULL
     assert f(NULL, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 0, NULL) == 1         # g NULL
     limit = 16 << 20
-    for rows, n in ((32768, 8192), (1 << 20, 16384), (497, 8192)):
+    for rows, n in ((32768, 16384), (1 << 20, 12288), (257, 16384)):
         assert lib.krsi_rmsnorm_bwd_workspace_bytes(rows, n) > limit
         for dt in (0, 1, 2):
             assert f(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, rows, n, dt, NULL) == TOO_LARGE
-    # The stated limit: every row count fits for n <= 7936, and n = 8192 fits up to 496 rows.
-    for rows, n in ((1 << 24, 7936), (496, 8192), (32768, 4096)):
+    # The stated limit: every row count fits for n <= 8192, and n = 16384 fits up to 256 rows.
+    for rows, n in ((1 << 24, 8192), (256, 16384), (32768, 4096)):
         assert lib.krsi_rmsnorm_bwd_workspace_bytes(rows, n) <= limit
     assert "16 MiB" in lib.krsi_error_string(TOO_LARGE).decode()
 

@@ -95,8 +95,8 @@ def test_rmsnorm_backward_deterministic():
 
 
 def test_rmsnorm_deterministic_at_config2_under_interleaved_work():
-    # a fixed grid of persistent workgroups writes dw partials that two
-    # column-sum launches reduce in a fixed order, so runs with unrelated GPU work in between
+    # a fixed grid of persistent workgroups writes dw partials that one
+    # column-sum launch reduces in a fixed order, so runs with unrelated GPU work in between
     # (which shifts which workgroups run where and when) agree bitwise.
     import _hip
 
