@@ -69,6 +69,12 @@ namespace {
 
 constexpr int kStep = 64;  // streamed positions per iteration
 
+// Start of the running max: the most negative finite float rather than -inf. A step whose
+// scores are all -inf (keys masked by -inf entries of the bias table) then gives p = exp2(-inf)
+// = 0 instead of exp2(-inf - -inf) = NaN; with any finite score the max, and every p, is the
+// same as from -inf (alpha = exp2(-FLT_MAX - m) = 0 = exp2(-inf)).
+constexpr float kMaxStart = -3.40282347e+38f;
+
 // Compile-time buffer index and tail flag for the unrolled step loops.
 constexpr std::integral_constant<int, 0> kBuf0{};
 constexpr std::integral_constant<int, 1> kBuf1{};
@@ -500,7 +506,7 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
   for (int db = 0; db < G::DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_run = -INFINITY, l_run[2] = {0.f, 0.f};
+  float m_run = kMaxStart, l_run[2] = {0.f, 0.f};
 
   uint32_t voff[Dma<DP, K::NT>::GPT];
   dma_offsets<DP, K::NT>(voff, ld, D);
@@ -614,7 +620,7 @@ __global__ __launch_bounds__(512, (DP == 64 ? 4 : 2)) void relpos_fwd_ks_kernel(
   for (int db = 0; db < G::DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_run = -INFINITY, l_run[2] = {0.f, 0.f};
+  float m_run = kMaxStart, l_run[2] = {0.f, 0.f};
 
   uint32_t voff[Dma<DP, K::NT>::GPT];
   dma_offsets<DP, K::NT>(voff, ld, D, gtid);
@@ -681,7 +687,7 @@ __global__ __launch_bounds__(512, (DP == 64 ? 4 : 2)) void relpos_fwd_ks_kernel(
     const float m1 = mine[0], l1 = mine[64];
     const float m = fmaxf(m_run, m1);
     const float a0 = __builtin_amdgcn_exp2f(m_run - m);
-    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+    const float a1 = __builtin_amdgcn_exp2f(m1 - m);  // 0 when group 1 saw no finite score
     const float lm[2] = {(l_run[0] + l_run[1]) * a0 + l1 * a1, 0.f};
 #pragma unroll
     for (int db = 0; db < G::DB; ++db)

@@ -196,7 +196,9 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
   f32x16 oacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = zero16();
-  float m_run = -INFINITY, l_run = 0.f;
+  // The most negative finite float, not -inf: a step whose scores are all -inf (keys masked by
+  // -inf bias entries) gives p = 0, not exp2(-inf - -inf) = NaN.
+  float m_run = -3.40282347e+38f, l_run = 0.f;
 
   const int T = (S + kStepF - 1) / kStepF;
   for (int t = 0; t < T; ++t) {
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);  // finite: key j0 < S is in every step
+    const float m_new = fmaxf(m_run, mx);
     const float alpha = exp2f(m_run - m_new);
     l_run *= alpha;
 #pragma unroll

@@ -110,12 +110,15 @@ def test_geglu_dtypes(dt, approximate, rows, f):
 
 
 # ------------------------------------------------ relative-position attention
-def _relpos_fp16(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_extra=0, seed=50):
+def _relpos_fp16(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_extra=0, seed=50,
+                 pd_fn=None, vs_eager=True):
     dt = torch.float16
     qkv = seeded((B * S, 3 * H * D + ld_extra), seed, std=std, dtype=dt)
     if ld_extra:
         qkv = qkv[:, :3 * H * D]
     pd = seeded((H, 2 * S - 1), seed + 1, std=pd_std, dtype=torch.float32)
+    if pd_fn is not None:
+        pd = pd_fn(pd)
     dout = seeded((B * S, H * D), seed + 2, dtype=dt)
     x = qkv.detach().requires_grad_(True)
     p = pd.detach().requires_grad_(True)
@@ -129,8 +132,9 @@ def _relpos_fp16(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_e
     kem = O.relpos_kernel_emulated(*a, dtype=dt)
     cand = (out.detach().to(dev), dqkv.to(dev), dpd.to(dev))
     tag = f"fp16 B{B} S{S} H{H} D{D}"
-    assert_parity(["out", "dqkv", "dpd"], (r[0], r[2], r[3]), (o[0], o[2], o[3]), cand,
-                  row_slack=float("inf"), extra_msg=tag + " vs eager fp16")
+    if vs_eager:
+        assert_parity(["out", "dqkv", "dpd"], (r[0], r[2], r[3]), (o[0], o[2], o[3]), cand,
+                      row_slack=float("inf"), extra_msg=tag + " vs eager fp16")
     assert_parity(["out", "dqkv", "dpd"], (r[0], r[2], r[3]), kem, cand,
                   extra_msg=tag + " vs reference-kernel rounding")
     _, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, scale)
@@ -163,12 +167,15 @@ def test_relpos_fp16_strided_and_large():
     _relpos_fp16(2, 1024, 16, 72, 1 / math.sqrt(72), ref_device="cuda")
 
 
-def _relpos_fp32(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_extra=0, seed=70):
+def _relpos_fp32(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_extra=0, seed=70,
+                 pd_fn=None):
     dt = torch.float32
     qkv = seeded((B * S, 3 * H * D + ld_extra), seed, std=std, dtype=dt)
     if ld_extra:
         qkv = qkv[:, :3 * H * D]
     pd = seeded((H, 2 * S - 1), seed + 1, std=pd_std, dtype=torch.float32)
+    if pd_fn is not None:
+        pd = pd_fn(pd)
     dout = seeded((B * S, H * D), seed + 2, dtype=dt)
     x = qkv.detach().requires_grad_(True)
     p = pd.detach().requires_grad_(True)
@@ -209,6 +216,26 @@ FP32_CASES = [  # B, S, H, D, scale, qkv std, pd std
 def test_relpos_fp32(B, S, H, D, scale, std, pd_std):
     log(f"relpos fp32 B{B} S{S} H{H} D{D} scale {scale:.4g}")
     _relpos_fp32(B, S, H, D, scale, std, pd_std)
+
+
+def _mask(kind, S):
+    """-inf entries of the table: keys after the query (causal) or more than 16 away (band16)."""
+    def fn(pd):
+        r = torch.arange(2 * S - 1, device=pd.device) - (S - 1)
+        keep = r <= 0 if kind == "causal" else r.abs() <= 16
+        return pd.masked_fill(~keep, float("-inf"))
+    return fn
+
+
+@pytest.mark.parametrize("mask", ["causal", "band16"])
+def test_relpos_fp16_fp32_masks_through_the_bias(mask):
+    """Masked relative positions in fp32 (against float64, with the eager fp32 yardstick) and
+    fp16 (against the reference kernel's rounding points, as the bf16 masked cases). band16
+    masks whole leading key steps of the later queries."""
+    log(f"relpos fp32 {mask} mask B2 S160 H2 D64")
+    _relpos_fp32(2, 160, 2, 64, 0.125, pd_std=0.5, pd_fn=_mask(mask, 160))
+    log(f"relpos fp16 {mask} mask B2 S160 H2 D64")
+    _relpos_fp16(2, 160, 2, 64, 0.125, pd_std=0.5, pd_fn=_mask(mask, 160), vs_eager=False)
 
 
 def test_relpos_fp32_single_position():
