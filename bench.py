@@ -8,7 +8,7 @@ timed on the host CPU beside it.
     python bench.py [--steps K] [--warmup W] [--only LIST] [--no-cpu] [--cpu-seconds S]
 
 LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, relpos_fp32, rmsnorm, geglu,
-geglu_linear, selftest_shapes, config1 (default: all).
+geglu_linear, selftest_shapes, config1, bucket (default: all).
 
 A "step" is one forward + backward pass of a kernel over one batch of synthetic input that is
 already resident in HBM (3 and 5; config 4 is the forward-only attention
@@ -433,6 +433,42 @@ def bench_selftest_shapes(args) -> dict:
     return res
 
 
+def bench_bucket(args) -> dict:
+    """The T5 bucketed table step either side of the attention at config 5's S and H: the gather
+    (table [32, H] -> pd [H, 2S-1]) and the bucket sum of dpd (dpd [H, 2S-1] -> dtable [32, H],
+    fixed order, no scatter), each against the torch ops that do the same step on the same GPU
+    (index_select, and index_add_, whose atomics make it non-deterministic). Launch-latency bound:
+    the bytes are a few MB."""
+    import _hip
+    import relpos_attention as A
+    S, H, nb = 4096, 16, 32
+    st = torch.cuda.current_stream()
+    table = _gen((nb, H), 1, dtype=torch.float32).cuda()
+    dpd = _gen((H, 2 * S - 1), 2, dtype=torch.float32).cuda()
+    bucket = A.t5_relative_position_bucket(S, True, nb, 128, table.device)
+    bl = bucket.long()
+    npd = H * (2 * S - 1)
+    work = {"gather": 4 * (2 * S - 1) + 4 * nb * H + 4 * npd, "sum": 4 * npd + 4 * (2 * S - 1) + 4 * nb * H}
+    legs = {
+        "gather": (lambda: _hip.relpos_bucket_gather(table, bucket, S),
+                   lambda: table.index_select(0, bl).t().contiguous()),
+        "sum": (lambda: _hip.relpos_bucket_sum(dpd, bucket, S, nb),
+                lambda: torch.zeros(nb, H, device=dpd.device).index_add_(0, bl, dpd.t())),
+    }
+    out = {}
+    for name, (ours, ref) in legs.items():
+        t = _time_steps(ours, args.steps, args.warmup, st)
+        r = _time_steps(ref, args.steps, args.warmup, st)
+        out[name] = {"us": round(t["ms_mean"] * 1e3, 2), "algorithmic_bytes": work[name],
+                     "GB/s": round(_rate(work[name], t["ms_mean"], 1e9), 1),
+                     "torch_ops_us": round(r["ms_mean"] * 1e3, 2)}
+    g = _hip.relpos_bucket_sum(dpd, bucket, S, nb)
+    ref = torch.zeros(nb, H, device=dpd.device, dtype=torch.float64).index_add_(0, bl, dpd.t().double())
+    out["sum_max_rel_err_vs_fp64"] = float(((g.double() - ref).abs().max() / ref.abs().max()).item())
+    return {"workload": f"T5 bucketed relative-position table, S {S}, H {H}, {nb} buckets (config 5's table step)",
+            "legs": out}
+
+
 def bench_config1(args) -> dict:
     """the RMSNorm forward the reference runs on its CPU path, x [2,1024,1152]
     and the ragged [1,300,1152]. The CPU figure (full size, no sampling) is the headline here;
@@ -556,7 +592,7 @@ def measured_copy_gbs() -> float:
     return round(2 * 2 * n / (ms * 1e-3) / 1e9, 1)
 
 
-ALL = "relpos,relpos_fwd,relpos_fp16,relpos_fp32,rmsnorm,geglu,geglu_linear,selftest_shapes,config1"
+ALL = "relpos,relpos_fwd,relpos_fp16,relpos_fp32,rmsnorm,geglu,geglu_linear,selftest_shapes,config1,bucket"
 
 
 def main() -> None:
@@ -596,6 +632,8 @@ def main() -> None:
         comps["selftest_shapes"] = bench_selftest_shapes(args)
     if "config1" in only:
         comps["rmsnorm_config1"] = bench_config1(args)
+    if "bucket" in only:
+        comps["relpos_bucket_table"] = bench_bucket(args)
     attach_traffic(comps)
     ceilings = {**attach_stream_ceiling(comps), **attach_gemm_ceiling(comps)}
     # The headline is config 5's attention; a run limited by --only to components without a
