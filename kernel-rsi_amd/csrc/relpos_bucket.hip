@@ -35,7 +35,9 @@ __global__ __launch_bounds__(kThreads) void bucket_gather(const float* __restric
 
 // Workgroup (b, h): thread t adds dpd[h, r] for r = t, t + 256, ... with
 // bucket[r] == b, in that order; the 256 partial sums are then added by a fixed
-// tree (wave-level shuffles, then the 4 wave sums in wave order).
+// tree (wave-level shuffles, then the 4 wave sums in wave order). Every entry is
+// loaded and the others add +0, so the loads do not wait on the compares; acc
+// starts at +0 and no sum rounds to -0, so adding +0 leaves it bitwise unchanged.
 __global__ __launch_bounds__(kThreads) void bucket_sum(const float* __restrict__ dpd,
                                                       const int32_t* __restrict__ bucket,
                                                       float* __restrict__ dtable, int npd, int H) {
@@ -43,8 +45,8 @@ __global__ __launch_bounds__(kThreads) void bucket_sum(const float* __restrict__
   const int b = blockIdx.x, h = blockIdx.y;
   const float* row = dpd + (int64_t)h * npd;
   float acc = 0.f;
-  for (int r = threadIdx.x; r < npd; r += kThreads)
-    if (bucket[r] == b) acc += row[r];
+#pragma unroll 8
+  for (int r = threadIdx.x; r < npd; r += kThreads) acc += bucket[r] == b ? row[r] : 0.f;
   acc = wave_sum(acc);
   if ((threadIdx.x & (kWave - 1)) == 0) s[threadIdx.x / kWave] = acc;
   __syncthreads();
