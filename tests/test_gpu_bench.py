@@ -1,6 +1,6 @@
 """bench.py's output contract on the GPU: one JSON line with the keys the driver reads, the
-roofline object and the measured ceilings. A short run: BASELINE config 4's forward only, no
-CPU baseline."""
+roofline object and the measured ceilings. Short runs with no CPU baseline: BASELINE config 4's
+forward, and a subset with no headline component."""
 import json
 import subprocess
 import sys
@@ -36,3 +36,18 @@ def test_bench_prints_one_contract_line():
     comp = line["components"]["relpos_attention_fwd_config4"]
     assert comp["gemm_ceiling"]["TFLOP/s"] > 0
     assert line["measured_peaks"]["gemm_bf16_TFLOP/s"] > 0
+
+
+def test_bench_subset_without_a_headline_component():
+    """--only config1 (and likewise selftest_shapes) has no single figure to head the line: the
+    line still prints, with value null and the component in place."""
+    log("bench: --only config1 --no-cpu --steps 2 --warmup 1")
+    p = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--only", "config1", "--no-cpu",
+                        "--steps", "2", "--warmup", "1"], capture_output=True, text=True, timeout=240, cwd=ROOT)
+    assert p.returncode == 0, p.stderr[-2000:]
+    lines = [ln for ln in p.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1, p.stdout[-2000:]
+    line = json.loads(lines[0])
+    assert line["value"] is None and line["roofline"] is None
+    shapes = line["components"]["rmsnorm_config1"]["shapes"]
+    assert all(s["gpu_fwd_us"] > 0 for s in shapes.values())
