@@ -72,19 +72,50 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// Rows p0 .. p0 + 63 of an [S, D] slice (row 0 at `base`, row stride ld floats) into a
-// staged tile; rows past S are zero. Columns [D, 32 DB) keep what zero_tile_pad wrote.
+// One step's tile rows held in registers between their global loads and their LDS stores, so
+// the loads of step t + 1 are in flight while step t computes. Thread t holds 16-byte chunks
+// t, t + 256, ... of the tile (at most 2 DB of them: D <= 32 DB). The stored tile holds rows
+// p0 .. p0 + 63 of the [S, D] slice at `base` (row stride ld floats), zero past S; columns
+// [D, 32 DB) keep what zero_tile_pad wrote. Every load reads a valid address (the last row,
+// masked, stands in for rows past S) so none waits behind a branch.
 template <int DB>
-__device__ __forceinline__ void stage_rows(float* tile, const float* base, int64_t ld, int p0, int S,
-                                           int D) {
-  const int cpr = D >> 2;
-  const int n = kStepF * cpr;
-  for (int c = threadIdx.x; c < n; c += kThreadsF) {
-    const int r = c / cpr, j = c - r * cpr;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (p0 + r < S) v = *reinterpret_cast<const f32x4*>(base + (int64_t)(p0 + r) * ld + 4 * j);
-    *reinterpret_cast<f32x4*>(tile + r * GeoF<DB>::LD + 4 * j) = v;
+struct TileRegs {
+  static constexpr int CPT = 2 * DB;
+  f32x4 v[CPT];
+  __device__ __forceinline__ void load(const float* base, int64_t ld, int p0, int S, int D) {
+    const int cpr = D >> 2, n = kStepF * cpr;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = min((int)threadIdx.x + k * kThreadsF, n - 1);
+      const int r = c / cpr, j = c - r * cpr;
+      const bool ok = (int)threadIdx.x + k * kThreadsF < n && p0 + r < S;
+      const int row = p0 + r < S ? p0 + r : S - 1;
+      f32x4 x = *reinterpret_cast<const f32x4*>(base + (int64_t)row * ld + 4 * j);
+      if (!ok) x = f32x4{0.f, 0.f, 0.f, 0.f};
+      v[k] = x;
+    }
   }
+  __device__ __forceinline__ void store(float* tile, int D) const {
+    const int cpr = D >> 2, n = kStepF * cpr;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = threadIdx.x + k * kThreadsF;
+      if (c < n) {
+        const int r = c / cpr, j = c - r * cpr;
+        *reinterpret_cast<f32x4*>(tile + r * GeoF<DB>::LD + 4 * j) = v[k];
+      }
+    }
+  }
+};
+
+// Bias window entry x = threadIdx.x (x < kWinF): pd[h, wb + x], zero outside [0, 2S - 1), loaded
+// into a register one step ahead.
+__device__ __forceinline__ float window_entry(const float* pdh, int npd, int wb) {
+  const int k = wb + (int)threadIdx.x;
+  return (threadIdx.x < (unsigned)kWinF && k >= 0 && k < npd) ? pdh[k] : 0.f;
+}
+__device__ __forceinline__ void store_window(float* bw, float v) {
+  if (threadIdx.x < (unsigned)kWinF) bw[threadIdx.x] = v;
 }
 
 template <int DB>
@@ -94,14 +125,6 @@ __device__ __forceinline__ void zero_tile_pad(float* tile, int D) {
   for (int c = threadIdx.x; c < kStepF * w; c += kThreadsF) {
     const int r = c / w;
     tile[r * LD + D + (c - r * w)] = 0.f;
-  }
-}
-
-// Window entry x (0 <= x < kWinF) = pd[h, wb + x], zero outside [0, 2S - 1).
-__device__ __forceinline__ void stage_window(float* bw, const float* pdh, int npd, int wb) {
-  for (int x = threadIdx.x; x < kWinF; x += kThreadsF) {
-    const int k = wb + x;
-    bw[x] = (k >= 0 && k < npd) ? pdh[k] : 0.f;
   }
 }
 
@@ -201,13 +224,23 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
   float m_run = -3.40282347e+38f, l_run = 0.f;
 
   const int T = (S + kStepF - 1) / kStepF;
+  const int wb0 = -i_wg - (kRowsF - 1) + S - 1;
+  TileRegs<DB> kn, vn;
+  kn.load(q0 + HD, ld, 0, S, D);
+  vn.load(q0 + 2 * HD, ld, 0, S, D);
+  float wn = window_entry(pdh, npd, wb0);
   for (int t = 0; t < T; ++t) {
     const int j0 = t * kStepF;
     __syncthreads();  // every wave is done with the previous step's tiles
-    stage_rows<DB>(Ks, q0 + HD, ld, j0, S, D);
-    stage_rows<DB>(Vs, q0 + 2 * HD, ld, j0, S, D);
-    stage_window(bw, pdh, npd, j0 - i_wg - (kRowsF - 1) + S - 1);
+    kn.store(Ks, D);
+    vn.store(Vs, D);
+    store_window(bw, wn);
     __syncthreads();
+    if (t + 1 < T) {  // step t + 1's loads, in flight while step t computes
+      kn.load(q0 + HD, ld, j0 + kStepF, S, D);
+      vn.load(q0 + 2 * HD, ld, j0 + kStepF, S, D);
+      wn = window_entry(pdh, npd, wb0 + j0 + kStepF);
+    }
     // Scores in log2 units, (q.k scale + bias) log2(e), keys past S at -inf; exact running max.
     f32x16 sc[2];
     float mx = -INFINITY;
@@ -300,13 +333,23 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dq_f32_kernel(
   for (int db = 0; db < DB; ++db) dq[db] = zero16();
 
   const int T = (S + kStepF - 1) / kStepF;
+  const int wb0 = -i_wg - (kRowsF - 1) + S - 1;
+  TileRegs<DB> kn, vn;
+  kn.load(q0 + HD, ld, 0, S, D);
+  vn.load(q0 + 2 * HD, ld, 0, S, D);
+  float wn = window_entry(pdh, npd, wb0);
   for (int t = 0; t < T; ++t) {
     const int j0 = t * kStepF;
     __syncthreads();
-    stage_rows<DB>(Ks, q0 + HD, ld, j0, S, D);
-    stage_rows<DB>(Vs, q0 + 2 * HD, ld, j0, S, D);
-    stage_window(bw, pdh, npd, j0 - i_wg - (kRowsF - 1) + S - 1);
+    kn.store(Ks, D);
+    vn.store(Vs, D);
+    store_window(bw, wn);
     __syncthreads();
+    if (t + 1 < T) {
+      kn.load(q0 + HD, ld, j0 + kStepF, S, D);
+      vn.load(q0 + 2 * HD, ld, j0 + kStepF, S, D);
+      wn = window_entry(pdh, npd, wb0 + j0 + kStepF);
+    }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       f32x16 s = dot_rows<DB>(Ks, kb * 32 + l32, g, ns, qr, zero16());
@@ -371,19 +414,37 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
   for (int db = 0; db < DB; ++db) dk[db] = dv[db] = zero16();
 
   const int T = (S + kStepF - 1) / kStepF;
+  // Window entry x = kk - iq + 63 holds pd[h, (j_wg + kk) - (i0 + iq) + S - 1].
+  const int wb0 = j_wg - (kStepF - 1) + S - 1;
+  TileRegs<DB> qn, on;
+  qn.load(q0, ld, 0, S, D);
+  on.load(o0, HD, 0, S, D);
+  float wn = window_entry(pdh, npd, wb0);
+  float ln = 0.f, dn = 0.f;  // lse and delta of query tid (threads tid < 64)
+  auto stats = [&](int i0) {
+    const int q = min(i0 + tid, S - 1);
+    ln = lse_bh[q];
+    dn = dl_bh[q];
+  };
+  stats(0);
   for (int t = 0; t < T; ++t) {
     const int i0 = t * kStepF;
     __syncthreads();
-    stage_rows<DB>(Qs, q0, ld, i0, S, D);
-    stage_rows<DB>(Os, o0, HD, i0, S, D);
-    // Window entry x = kk - iq + 63 holds pd[h, (j_wg + kk) - (i0 + iq) + S - 1].
-    stage_window(bw, pdh, npd, j_wg - i0 - (kStepF - 1) + S - 1);
+    qn.store(Qs, D);
+    on.store(Os, D);
+    store_window(bw, wn);
     if (tid < kStepF) {
       const bool ok = i0 + tid < S;
-      Lq[tid] = ok ? lse_bh[i0 + tid] : INFINITY;  // queries past S: p = 0
-      Dq[tid] = ok ? dl_bh[i0 + tid] : 0.f;
+      Lq[tid] = ok ? ln : INFINITY;  // queries past S: p = 0
+      Dq[tid] = ok ? dn : 0.f;
     }
     __syncthreads();
+    if (t + 1 < T) {
+      qn.load(q0, ld, i0 + kStepF, S, D);
+      on.load(o0, HD, i0 + kStepF, S, D);
+      wn = window_entry(pdh, npd, wb0 - i0 - kStepF);
+      stats(i0 + kStepF);
+    }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       // S and dP [query][key]: rows are this step's queries, columns the lane's key.
