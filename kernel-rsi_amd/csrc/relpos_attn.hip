@@ -457,6 +457,56 @@ __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const
   if (g == 0) *lse_q = m_run + log2f(l);
 }
 
+// The same outputs stored through a wave-private LDS tile `wt` (32 rows x kStoreLd floats), one
+// 32-column head-dim block at a time, so each global store instruction writes whole row segments
+// (8 lanes per 128-byte fp32 row block, 4 lanes per 64-byte bf16 one) instead of 16 or 8 bytes
+// in each of 32 rows. Every lane of the wave must call it; rows >= nrows are not stored. row0:
+// element offset of the wave's first row (head h's columns), HD: row stride.
+constexpr int kStoreLd = 36;  // tile row stride in floats: 16 rows of one column hit 16 bank quads
+template <int DT, int DP>
+__device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run, const float* l_run,
+                                                 int lane, int nrows, int64_t row0, int64_t HD, int D,
+                                                 uint16_t* __restrict__ out, float* __restrict__ out32,
+                                                 float* __restrict__ lse_q, float* wt) {
+  const int g = lane >> 5, l32 = lane & 31;
+  const float l = xhalf_sum(l_run[0] + l_run[1]);
+  if (g == 0 && l32 < nrows) *lse_q = m_run + log2f(l);
+#pragma unroll
+  for (int db = 0; db < Geo<DP>::DB; ++db) {
+    const int ncol = min(32, D - 32 * db);  // a multiple of 8
+    if (ncol <= 0) break;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      f32x4 o;
+#pragma unroll
+      for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
+      *reinterpret_cast<f32x4*>(wt + l32 * kStoreLd + 8 * a + 4 * g) = o;
+    }
+    // Other lanes' values are read back: keep every tile write of this block before the reads
+    // (the LDS executes one wave's operations in order).
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // fp32: 32 rows x 8 chunks of 4
+      const int c = lane + 64 * k, r = c >> 3, j = c & 7;
+      if (r < nrows && 4 * j < ncol)
+        *reinterpret_cast<f32x4*>(out32 + row0 + r * HD + 32 * db + 4 * j) =
+            *reinterpret_cast<const f32x4*>(wt + r * kStoreLd + 4 * j);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // activation dtype: 32 rows x 4 chunks of 8
+      const int c = lane + 64 * k, r = c >> 2, j = c & 3;
+      if (r < nrows && 8 * j < ncol) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(wt + r * kStoreLd + 8 * j);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(wt + r * kStoreLd + 8 * j + 4);
+        const u32x4 v = {Elem<DT>::pack2(x[0], x[1]), Elem<DT>::pack2(x[2], x[3]), Elem<DT>::pack2(y[0], y[1]),
+                         Elem<DT>::pack2(y[2], y[3])};
+        *reinterpret_cast<u32x4*>(out + row0 + r * HD + 32 * db + 8 * j) = v;
+      }
+    }
+    asm volatile("" ::: "memory");  // the next block's writes after these reads
+  }
+}
+
 // At head dims 49-64 (DP = 64) the forward runs 4 waves per SIMD (128 VGPRs; spills only in the
 // prologue and the last step): more waves give one wave's VALU softmax more MFMA work of the
 // others to overlap with (-2% at config 5 against 3 waves).
@@ -469,9 +519,11 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
   using K = Blk<NW>;
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * TILE];
+  // K tiles, then V tiles (one array, so the output staging can reuse all of it).
+  __shared__ __attribute__((aligned(16))) uint16_t KVs[4 * TILE];
   __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
+  uint16_t* const Ks = KVs;
+  uint16_t* const Vs = KVs + 2 * TILE;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
@@ -550,8 +602,16 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
       step(t, kBuf0, kTail);
   }
 
-  fwd_store<DT, DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
-                lse + (int64_t)bh * S + qi);
+  constexpr int kWaveTile = 32 * kStoreLd;  // floats
+  if constexpr (NW * kWaveTile * 4 <= (int)sizeof(KVs)) {
+    __syncthreads();  // every wave is done with the last tiles
+    fwd_store_staged<DT, DP>(oacc, m_run, l_run, lane, min(32, S - (i_wg + wave * 32)),
+                             (tok0 + i_wg + wave * 32) * HD + (int64_t)h * D, HD, D, out, out32,
+                             lse + (int64_t)bh * S + qi, reinterpret_cast<float*>(KVs) + wave * kWaveTile);
+  } else {
+    fwd_store<DT, DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
+                      lse + (int64_t)bh * S + qi);
+  }
 }
 
 // ------------------------------------------- forward, keys split inside the workgroup
@@ -566,7 +626,7 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
 // half keeps its own exact running max, so p of the second half is rounded relative to that
 // half's maximum rather than to the running maximum over all earlier keys.
 template <int DT, int DP>
-__global__ __launch_bounds__(512, (DP == 64 ? 4 : 2)) void relpos_fwd_ks_kernel(
+__global__ __launch_bounds__(512, (DP == 64 || DP <= 32 ? 4 : 2)) void relpos_fwd_ks_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
     int D, Fold f) {
@@ -693,8 +753,12 @@ __global__ __launch_bounds__(512, (DP == 64 ? 4 : 2)) void relpos_fwd_ks_kernel(
     for (int db = 0; db < G::DB; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * a0 + mine[(2 + 16 * db + r) * 64] * a1;
-    fwd_store<DT, DP>(oacc, m, lm, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
-                      lse + (int64_t)bh * S + qi);
+    // The wave's hand-over rows, all read above, become its output staging tile.
+    static_assert(32 * kStoreLd <= SLOTS * 64, "the staging tile fits a wave's hand-over rows");
+    asm volatile("" ::: "memory");
+    fwd_store_staged<DT, DP>(oacc, m, lm, lane, min(32, S - (i_wg + gw * 32)),
+                             (tok0 + i_wg + gw * 32) * HD + (int64_t)h * D, HD, D, out, out32,
+                             lse + (int64_t)bh * S + qi, reinterpret_cast<float*>(stage) + (gw * SLOTS) * 64);
   }
 }
 
