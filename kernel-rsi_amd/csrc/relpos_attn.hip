@@ -457,20 +457,19 @@ __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const
   if (g == 0) *lse_q = m_run + log2f(l);
 }
 
-// The same outputs stored through a wave-private LDS tile `wt` (32 rows x kStoreLd floats), one
-// 32-column head-dim block at a time, so each global store instruction writes whole row segments
-// (8 lanes per 128-byte fp32 row block, 4 lanes per 64-byte bf16 one) instead of 16 or 8 bytes
-// in each of 32 rows. Every lane of the wave must call it; rows >= nrows are not stored. row0:
-// element offset of the wave's first row (head h's columns), HD: row stride.
+// Staged stores. A wave's transposed accumulators (lane l32 holds row l32; register 4a + b4 of
+// block db holds column 32db + 8a + 4g + b4) go through a wave-private LDS tile `wt` (32 rows x
+// kStoreLd floats), one 32-column block at a time, so each global store instruction writes whole
+// row segments (8 lanes per 128-byte fp32 row block, 4 lanes per 64-byte 16-bit one) instead of
+// 16 or 8 bytes in each of 32 rows. Every lane of the wave must call them; rows >= nrows are not
+// stored. row0: element offset of the wave's first row; rstride: row stride in elements.
 constexpr int kStoreLd = 36;  // tile row stride in floats: 16 rows of one column hit 16 bank quads
-template <int DT, int DP>
-__device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run, const float* l_run,
-                                                 int lane, int nrows, int64_t row0, int64_t HD, int D,
-                                                 uint16_t* __restrict__ out, float* __restrict__ out32,
-                                                 float* __restrict__ lse_q, float* wt) {
+constexpr int kWaveTile = 32 * kStoreLd;  // floats per wave
+template <int DT, int DP, bool W32, typename Op>
+__device__ __forceinline__ void store_rows_staged(const f32x16* acc, Op op, int lane, int nrows, int64_t row0,
+                                                  int64_t rstride, int D, uint16_t* __restrict__ out,
+                                                  float* __restrict__ out32, float* wt) {
   const int g = lane >> 5, l32 = lane & 31;
-  const float l = xhalf_sum(l_run[0] + l_run[1]);
-  if (g == 0 && l32 < nrows) *lse_q = m_run + log2f(l);
 #pragma unroll
   for (int db = 0; db < Geo<DP>::DB; ++db) {
     const int ncol = min(32, D - 32 * db);  // a multiple of 8
@@ -479,18 +478,20 @@ __device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run
     for (int a = 0; a < 4; ++a) {
       f32x4 o;
 #pragma unroll
-      for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
+      for (int b4 = 0; b4 < 4; ++b4) o[b4] = op(acc[db][4 * a + b4]);
       *reinterpret_cast<f32x4*>(wt + l32 * kStoreLd + 8 * a + 4 * g) = o;
     }
     // Other lanes' values are read back: keep every tile write of this block before the reads
     // (the LDS executes one wave's operations in order).
     asm volatile("" ::: "memory");
+    if constexpr (W32) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {  // fp32: 32 rows x 8 chunks of 4
-      const int c = lane + 64 * k, r = c >> 3, j = c & 7;
-      if (r < nrows && 4 * j < ncol)
-        *reinterpret_cast<f32x4*>(out32 + row0 + r * HD + 32 * db + 4 * j) =
-            *reinterpret_cast<const f32x4*>(wt + r * kStoreLd + 4 * j);
+      for (int k = 0; k < 4; ++k) {  // fp32: 32 rows x 8 chunks of 4
+        const int c = lane + 64 * k, r = c >> 3, j = c & 7;
+        if (r < nrows && 4 * j < ncol)
+          *reinterpret_cast<f32x4*>(out32 + row0 + r * rstride + 32 * db + 4 * j) =
+              *reinterpret_cast<const f32x4*>(wt + r * kStoreLd + 4 * j);
+      }
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {  // activation dtype: 32 rows x 4 chunks of 8
@@ -500,11 +501,23 @@ __device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run
         const f32x4 y = *reinterpret_cast<const f32x4*>(wt + r * kStoreLd + 8 * j + 4);
         const u32x4 v = {Elem<DT>::pack2(x[0], x[1]), Elem<DT>::pack2(x[2], x[3]), Elem<DT>::pack2(y[0], y[1]),
                          Elem<DT>::pack2(y[2], y[3])};
-        *reinterpret_cast<u32x4*>(out + row0 + r * HD + 32 * db + 8 * j) = v;
+        *reinterpret_cast<u32x4*>(out + row0 + r * rstride + 32 * db + 8 * j) = v;
       }
     }
     asm volatile("" ::: "memory");  // the next block's writes after these reads
   }
+}
+
+// Forward outputs: O = acc / l (fp32 and the activation dtype), lse = m + log2 l.
+template <int DT, int DP>
+__device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run, const float* l_run,
+                                                 int lane, int nrows, int64_t row0, int64_t HD, int D,
+                                                 uint16_t* __restrict__ out, float* __restrict__ out32,
+                                                 float* __restrict__ lse_q, float* wt) {
+  const float l = xhalf_sum(l_run[0] + l_run[1]);
+  if ((lane >> 5) == 0 && (lane & 31) < nrows) *lse_q = m_run + log2f(l);
+  store_rows_staged<DT, DP, true>(oacc, [l](float x) { return x / l; }, lane, nrows, row0, HD, D, out, out32,
+                                  wt);
 }
 
 // At head dims 49-64 (DP = 64) the forward runs 4 waves per SIMD (128 VGPRs; spills only in the
@@ -602,7 +615,6 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
       step(t, kBuf0, kTail);
   }
 
-  constexpr int kWaveTile = 32 * kStoreLd;  // floats
   if constexpr (NW * kWaveTile * 4 <= (int)sizeof(KVs)) {
     __syncthreads();  // every wave is done with the last tiles
     fwd_store_staged<DT, DP>(oacc, m_run, l_run, lane, min(32, S - (i_wg + wave * 32)),
@@ -812,9 +824,11 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   using K = Blk<NW>;
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2 * TILE];
+  // K tiles, then V tiles (one array, so the dQ staging can reuse all of it).
+  __shared__ __attribute__((aligned(16))) uint16_t KVs[4 * TILE];
   __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
+  uint16_t* const Ks = KVs;
+  uint16_t* const Vs = KVs + 2 * TILE;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
@@ -910,7 +924,12 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
       step(t, kBuf0, kTail);
   }
 
-  if (qvalid) {
+  if constexpr (NW * kWaveTile * 4 <= (int)sizeof(KVs)) {
+    __syncthreads();  // every wave is done with the last tiles
+    store_rows_staged<DT, DP, false>(dq, [scale](float x) { return x * scale; }, lane,
+                                     min(32, S - (i_wg + wave * 32)), (tok0 + i_wg + wave * 32) * ldd + (int64_t)h * D,
+                                     ldd, D, dqkv, nullptr, reinterpret_cast<float*>(KVs) + wave * kWaveTile);
+  } else if (qvalid) {
     const int64_t qbase = (tok0 + qi) * ldd + (int64_t)h * D;
 #pragma unroll
     for (int db = 0; db < G::DB; ++db)
@@ -955,6 +974,39 @@ __device__ __forceinline__ int ring_base(int wg, int k, int off1) {
   return (2 * wg + k) * kRingSlots + 4 * wg + (k ? off1 : 0);
 }
 __device__ __forceinline__ int kperm(int l) { return 2 * (l & 15) + (l >> 4); }
+
+// Staged store of a dK or dV accumulator (lane l32 holds head dim 32db + l32; register r holds
+// tile row 8(r/4) + 4g + r%4, i.e. key kperm(row) of the wave): each 32-column block goes into
+// the wave-private tile `wt` as [key][dim] (32 consecutive floats per half-wave write: no bank
+// conflict), then whole row segments are stored, 4 lanes per 64-byte row block, instead of one
+// 16-bit value per lane. Rows (keys) >= nrows are not stored. Every lane of the wave must call it.
+constexpr int kColLd = 40;                // tile row stride in floats
+constexpr int kColTile = 32 * kColLd;     // floats per wave
+template <int DT, int DP, typename Op>
+__device__ __forceinline__ void store_cols_staged(const f32x16* acc, Op op, int lane, int nrows, int64_t row0,
+                                                  int64_t rstride, int D, uint16_t* __restrict__ out, float* wt) {
+  const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int db = 0; db < Geo<DP>::DB; ++db) {
+    const int ncol = min(32, D - 32 * db);  // a multiple of 8
+    if (ncol <= 0) break;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) wt[kperm(8 * (r >> 2) + 4 * g + (r & 3)) * kColLd + l32] = op(acc[db][r]);
+    asm volatile("" ::: "memory");  // the writes before the other lanes' reads
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // 32 rows x 4 chunks of 8
+      const int c = lane + 64 * k, r = c >> 2, j = c & 3;
+      if (r < nrows && 8 * j < ncol) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(wt + r * kColLd + 8 * j);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(wt + r * kColLd + 8 * j + 4);
+        const u32x4 v = {Elem<DT>::pack2(x[0], x[1]), Elem<DT>::pack2(x[2], x[3]), Elem<DT>::pack2(y[0], y[1]),
+                         Elem<DT>::pack2(y[2], y[3])};
+        *reinterpret_cast<u32x4*>(out + row0 + r * rstride + 32 * db + 8 * j) = v;
+      }
+    }
+    asm volatile("" ::: "memory");  // the next block's writes after these reads
+  }
+}
 
 __device__ __forceinline__ float quad_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
@@ -1182,17 +1234,26 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 
   // D layout: lane = head dim d (n), register r = tile row 8(r/4) + 4g + r%4, which holds
   // key kperm(row) of this wave.
+  if constexpr (2 * kColTile * 4 <= (int)sizeof(Qs)) {
+    // Staged: waves 0-1 in the Q tiles, 2-3 in the dO tiles (free since the fold's barrier).
+    float* wt = reinterpret_cast<float*>(wave < 2 ? Qs : Os) + (wave & 1) * kColTile;
+    const int nrows = min(32, S - (j_wg + wave * 32));
+    const int64_t row0 = (tok0 + j_wg + wave * 32) * ldd + HD + (int64_t)h * D;
+    store_cols_staged<DT, DP>(dk, [scale](float x) { return x * scale; }, lane, nrows, row0, ldd, D, dqkv, wt);
+    store_cols_staged<DT, DP>(dv, [](float x) { return x; }, lane, nrows, row0 + HD, ldd, D, dqkv, wt);
+  } else {
 #pragma unroll
-  for (int db = 0; db < G::DB; ++db) {
-    const int d = db * 32 + l32;
-    if (d < D) {
+    for (int db = 0; db < G::DB; ++db) {
+      const int d = db * 32 + l32;
+      if (d < D) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = j_wg + wave * 32 + kperm(8 * (r >> 2) + 4 * g + (r & 3));
-        if (key < S) {
-          uint16_t* rowp = dqkv + (tok0 + key) * ldd + HD + (int64_t)h * D + d;
-          rowp[0] = Elem<DT>::store(dk[db][r] * scale);
-          rowp[HD] = Elem<DT>::store(dv[db][r]);
+        for (int r = 0; r < 16; ++r) {
+          const int key = j_wg + wave * 32 + kperm(8 * (r >> 2) + 4 * g + (r & 3));
+          if (key < S) {
+            uint16_t* rowp = dqkv + (tok0 + key) * ldd + HD + (int64_t)h * D + d;
+            rowp[0] = Elem<DT>::store(dk[db][r] * scale);
+            rowp[HD] = Elem<DT>::store(dv[db][r]);
+          }
         }
       }
     }
