@@ -231,10 +231,13 @@ def test_relpos_rejects_bad_input():
         A.relpos_attention(q2, seeded((1, 15), 1, dtype=torch.float32), 1, 8, 1, 12, 0.125)  # D % 8
 
 
-@pytest.mark.parametrize("B,S,H,D", [(4, 2048, 8, 128), (4, 1024, 16, 72), (4, 4096, 4, 32)])
+@pytest.mark.parametrize("B,S,H,D", [(4, 2048, 8, 128), (4, 1024, 16, 72), (4, 4096, 4, 32), (2, 300, 128, 64),
+                                     (1, 333, 256, 72)])
 def test_relpos_large_grid_head_dims(B, S, H, D):
     """Grids of 512+ forward workgroups take the 4-wave forward (smaller grids split keys over
-    two wave groups, which the small cases above exercise): head dims other than 64 there."""
+    two wave groups, which the small cases above exercise): head dims other than 64 there, and
+    ragged S, whose last query block has waves wholly past S and one partly past it (the
+    staged output store skips those rows)."""
     assert (S + 127) // 128 * B * H >= 512
     log(f"relpos large grid B{B} S{S} H{H} D{D}")
     _check(B, S, H, D, 1 / math.sqrt(D), ref_device="cuda")
