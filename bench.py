@@ -606,7 +606,7 @@ def main() -> None:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's kernels run on one MI355X and no "
-              "multi-GPU figure is produced (see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "multi-GPU figure is produced; run it with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
