@@ -1,7 +1,6 @@
 """The C-ABI boundary without a GPU: the library loads, exports every entry point of
 include/krsi.h with the declared signature, binds to torch's HIP runtime, reports errors
 for invalid arguments before launching anything, and the Python layer has no CPU path."""
-import ctypes
 import re
 from pathlib import Path
 
