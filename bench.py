@@ -7,8 +7,8 @@ timed on the host CPU beside it.
 
     python bench.py [--steps K] [--warmup W] [--only LIST] [--no-cpu] [--cpu-seconds S]
 
-LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, relpos_fp32, rmsnorm, geglu,
-geglu_linear, selftest_shapes, config1, bucket (default: all).
+LIST is comma-separated from: relpos, relpos_fwd, relpos_fp16, relpos_fp32, relpos_long, rmsnorm,
+geglu, geglu_linear, selftest_shapes, config1, bucket (default: all).
 
 A "step" is one forward + backward pass of a kernel over one batch of synthetic input that is
 already resident in HBM (3 and 5; config 4 is the forward-only attention
@@ -350,6 +350,39 @@ def bench_relpos(args, B=4, S=4096, H=16, D=64, dtype=torch.bfloat16) -> dict:
     return res
 
 
+def bench_relpos_long(args) -> dict:
+    """Long context, B1 H16 L16384 D64 bf16 fwd+bwd (not a BASELINE config; parity-tested at this
+    S): the dpd diagonal sums are formed inside the dK/dV kernel, so the backward's workspace is
+    B*H*ceil(L/128)*(L+128) fp32 partial rows instead of the reference's [B, H, L, L] fp32 dbias.
+    Two input sets (0.4 GB with their outputs), backward lagging the forward by one."""
+    import _hip
+    B, S, H, D = 1, 16384, 16, 64
+    scale = 1.0 / math.sqrt(D)
+    nset, lag = 2, 1
+    qkv_dev = [_gen((B * S, 3 * H * D), 300 + i).cuda() for i in range(nset)]
+    dout_dev = [_gen((B * S, H * D), 400 + i).cuda() for i in range(nset)]
+    pd = _gen((H, 2 * S - 1), 1, std=0.02, dtype=torch.float32).cuda()
+    st = torch.cuda.current_stream()
+    saved = [_hip.relpos_fwd(q, pd, B, S, H, D, scale)[1:] for q in qkv_dev]
+
+    def fwd(i):
+        saved[i] = _hip.relpos_fwd(qkv_dev[i], pd, B, S, H, D, scale)[1:]
+
+    def bwd(i):
+        _hip.relpos_bwd(dout_dev[i], qkv_dev[i], pd, *saved[i], B, S, H, D, scale)
+
+    total = 14 * B * H * S * S * D
+    t = _time_steps(_pipelined(fwd, bwd, nset, lag), args.steps, args.warmup, st)
+    tfl = _rate(total, t["ms_mean"], 1e12)
+    return {"workload": f"relpos attention fwd+bwd B{B} H{H} L{S} D{D} bf16 (long context)",
+            "value": round(tfl, 2), "unit": "TFLOP/s", "ms_per_step": round(t["ms_mean"], 4),
+            "algorithmic_flops": total, "matrix_dtype": "bf16",
+            "rotation": f"{nset} input sets (qkv, dout), backward lags forward by {lag}",
+            "bwd_workspace_bytes": int(_hip.lib().krsi_relpos_bwd_workspace_bytes(B, S, H, D)),
+            "reference_dbias_bytes": 4 * B * H * S * S,
+            "roofline": _roofline(tfl, "TFLOP/s")}
+
+
 def bench_relpos_fwd_config4(args) -> dict:
     import _hip
     B, S, H, D = 2, 1024, 16, 72
@@ -592,7 +625,8 @@ def measured_copy_gbs() -> float:
     return round(2 * 2 * n / (ms * 1e-3) / 1e9, 1)
 
 
-ALL = "relpos,relpos_fwd,relpos_fp16,relpos_fp32,rmsnorm,geglu,geglu_linear,selftest_shapes,config1,bucket"
+ALL = ("relpos,relpos_fwd,relpos_fp16,relpos_fp32,relpos_long,rmsnorm,geglu,geglu_linear,selftest_shapes,config1,"
+       "bucket")
 
 
 def main() -> None:
@@ -622,6 +656,8 @@ def main() -> None:
         comps["relpos_attention_fp16"] = bench_relpos(args, dtype=torch.float16)
     if "relpos_fp32" in only:
         comps["relpos_attention_fp32"] = bench_relpos(args, B=2, S=1024, H=16, D=72, dtype=torch.float32)
+    if "relpos_long" in only:
+        comps["relpos_attention_long"] = bench_relpos_long(args)
     if "rmsnorm" in only:
         comps["rmsnorm"] = bench_rmsnorm(args)
     if "geglu" in only:
