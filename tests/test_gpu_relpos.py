@@ -141,6 +141,12 @@ def test_relpos_fwd_config4():
     _check(2, 1024, 16, 72, 1 / math.sqrt(72), ref_device="cuda")
 
 
+def test_relpos_fwd_config4_ragged():
+    """BASELINE config 4's ragged case at its full width: B2 H16 L300 D72 (fwd; bwd checked too)."""
+    log("relpos config4 ragged B2 S300 H16 D72")
+    _check(2, 300, 16, 72, 1 / math.sqrt(72), ref_device="cuda")
+
+
 def test_relpos_train_config5():
     """B4 H16 L4096 D64 fwd+bwd, dq/dk/dv and the bias-table gradient."""
     log("relpos config5 B4 S4096 H16 D64")
