@@ -7,10 +7,10 @@
 // The reference's note on this step (LESSONS.md:35): the embedding backward is a
 // contended scatter-add over S^2 indices; summing dBias along the diagonals into
 // the per-distance table [H, 2S-1] (the attention backward does that) and then
-// into the buckets needs no scatter. Here the bucket sum is a gather as well:
-// workgroup (b, h) reads the whole bucket map and adds its own entries in a fixed
-// order, so dtable is bitwise reproducible with no atomics. The map is 2S-1 int32
-// (32 KB at S = 4096) and stays in L2 for all num_buckets x H workgroups.
+// into the buckets needs no scatter. Here the bucket sum is a gather as well: each
+// workgroup reads the whole bucket map for one head and a few buckets and adds their
+// entries in a fixed order, so dtable is bitwise reproducible with no atomics. The map
+// is 2S-1 int32 (32 KB at S = 4096) and stays in L2 for all the workgroups.
 #include "krsi_device.h"
 #include "krsi_internal.h"
 
@@ -33,24 +33,44 @@ __global__ __launch_bounds__(kThreads) void bucket_gather(const float* __restric
   pd[(int64_t)h * npd + r] = (b >= 0 && b < nb) ? table[(int64_t)b * H + h] : __builtin_nanf("");
 }
 
-// Workgroup (b, h): thread t adds dpd[h, r] for r = t, t + 256, ... with
-// bucket[r] == b, in that order; the 256 partial sums are then added by a fixed
-// tree (wave-level shuffles, then the 4 wave sums in wave order). Every entry is
-// loaded and the others add +0, so the loads do not wait on the compares; acc
-// starts at +0 and no sum rounds to -0, so adding +0 leaves it bitwise unchanged.
+// Workgroup (g, h) sums buckets b = g NBW + k, k < NBW (those below nb): thread t adds
+// dpd[h, r] for r = t, t + 256, ... with bucket[r] == b, in that order, into its own sum per
+// bucket, each entry and bucket id loaded once for all NBW buckets; each bucket's 256 partial
+// sums are then added by a fixed tree (wave-level shuffles, then the 4 wave sums in wave
+// order). Every entry is added to every sum, as +0 where the bucket differs, so the loads do
+// not wait on the compares; a sum starts at +0 and no sum rounds to -0, so adding +0 leaves it
+// bitwise unchanged: each bucket's result does not depend on NBW. The entry is loaded ahead of
+// the compares, so no load waits behind one (the earlier `bucket[r] == b ? row[r] : 0` form took
+// 6.9 us at S 4096, H 16, 32 buckets; this one 3.8 us with NBW = 1, 4.0 / 4.7 / 6.5 us with NBW =
+// 2 / 4 / 8; at S <= 1024 every NBW takes 3.8-4.0 us, the launch floor).
+constexpr int kBucketsPerWg = 1;
+template <int NBW>
 __global__ __launch_bounds__(kThreads) void bucket_sum(const float* __restrict__ dpd,
                                                       const int32_t* __restrict__ bucket,
-                                                      float* __restrict__ dtable, int npd, int H) {
-  __shared__ float s[kThreads / kWave];
-  const int b = blockIdx.x, h = blockIdx.y;
+                                                      float* __restrict__ dtable, int npd, int H, int nb) {
+  __shared__ float s[NBW][kThreads / kWave];
+  const int b0 = blockIdx.x * NBW, h = blockIdx.y;
   const float* row = dpd + (int64_t)h * npd;
-  float acc = 0.f;
+  float acc[NBW];
+#pragma unroll
+  for (int k = 0; k < NBW; ++k) acc[k] = 0.f;
 #pragma unroll 8
-  for (int r = threadIdx.x; r < npd; r += kThreads) acc += bucket[r] == b ? row[r] : 0.f;
-  acc = wave_sum(acc);
-  if ((threadIdx.x & (kWave - 1)) == 0) s[threadIdx.x / kWave] = acc;
+  for (int r = threadIdx.x; r < npd; r += kThreads) {
+    const int br = bucket[r];
+    const float v = row[r];
+#pragma unroll
+    for (int k = 0; k < NBW; ++k) acc[k] += br == b0 + k ? v : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < NBW; ++k) {
+    const float w = wave_sum(acc[k]);
+    if ((threadIdx.x & (kWave - 1)) == 0) s[k][threadIdx.x / kWave] = w;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) dtable[(int64_t)b * H + h] = ((s[0] + s[1]) + s[2]) + s[3];
+  if (threadIdx.x < NBW && b0 + (int)threadIdx.x < nb) {
+    const int k = threadIdx.x;
+    dtable[(int64_t)(b0 + k) * H + h] = ((s[k][0] + s[k][1]) + s[k][2]) + s[k][3];
+  }
 }
 
 int check_bucket(int S, int H, int nb) {
@@ -83,8 +103,9 @@ int krsi_relpos_bucket_sum(const float* dpd, const int32_t* bucket, float* dtabl
   int rc = check_bucket(S, H, num_buckets);
   if (rc != KRSI_OK) return rc;
   if (!dpd || !bucket || !dtable) return KRSI_ERR_NULL_POINTER;
-  hipLaunchKernelGGL(bucket_sum, dim3((unsigned)num_buckets, (unsigned)H), dim3(kThreads), 0,
-                     as_stream(stream), dpd, bucket, dtable, 2 * S - 1, (int)H);
+  hipLaunchKernelGGL(bucket_sum<kBucketsPerWg>, dim3((unsigned)ceil_div(num_buckets, kBucketsPerWg), (unsigned)H),
+                     dim3(kThreads), 0, as_stream(stream), dpd, bucket, dtable, 2 * S - 1, (int)H,
+                     (int)num_buckets);
   return launch_status();
 }
 
