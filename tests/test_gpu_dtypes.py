@@ -279,3 +279,13 @@ def test_relpos_fp16_config5_shape():
     GPU, with the same two criteria as the small cases."""
     log("relpos fp16 B4 S4096 H16 D64")
     _relpos_fp16(4, 4096, 16, 64, 1 / 8, ref_device="cuda")
+
+
+@pytest.mark.parametrize("S", [8191, 16384])
+def test_relpos_fp16_fp32_long_sequence(S):
+    """Long context in fp16 and fp32 (B1 H2 D64), against the fp32 reference on the GPU: the odd
+    S = 8191 takes the scalar dpd reduce, S = 16384 the 128-bit one, as in bf16."""
+    log(f"relpos fp16 long context B1 S{S} H2 D64")
+    _relpos_fp16(1, S, 2, 64, 0.125, ref_device="cuda")
+    log(f"relpos fp32 long context B1 S{S} H2 D64")
+    _relpos_fp32(1, S, 2, 64, 0.125, ref_device="cuda")
