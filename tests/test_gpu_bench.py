@@ -1,6 +1,6 @@
 """bench.py's output contract on the GPU: one JSON line with the keys the driver reads, the
 roofline object and the measured ceilings. Short runs with no CPU baseline: BASELINE config 4's
-forward, and a subset with no headline component."""
+forward, a subset with no headline component, and the long-context attention line."""
 import json
 import subprocess
 import sys
@@ -51,3 +51,17 @@ def test_bench_subset_without_a_headline_component():
     assert line["value"] is None and line["roofline"] is None
     shapes = line["components"]["rmsnorm_config1"]["shapes"]
     assert all(s["gpu_fwd_us"] > 0 for s in shapes.values())
+
+
+def test_bench_long_context_leg():
+    """--only relpos_long: the long-context attention line, whose backward workspace (dpd partial
+    rows) is a small fraction of the reference's [B, H, S, S] fp32 dbias."""
+    log("bench: --only relpos_long --no-cpu --steps 2 --warmup 1")
+    p = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--only", "relpos_long", "--no-cpu",
+                        "--steps", "2", "--warmup", "1"], capture_output=True, text=True, timeout=240, cwd=ROOT)
+    assert p.returncode == 0, p.stderr[-2000:]
+    lines = [ln for ln in p.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1, p.stdout[-2000:]
+    comp = json.loads(lines[0])["components"]["relpos_attention_long"]
+    assert comp["value"] > 0 and comp["unit"] == "TFLOP/s"
+    assert 0 < comp["bwd_workspace_bytes"] < comp["reference_dbias_bytes"] / 100
