@@ -374,7 +374,10 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta_ws,
     float* __restrict__ dqkv, int64_t ldd, float* __restrict__ part, int S, int H, int D, float scale) {
   using G = GeoF<DB>;
-  constexpr int DSL = kRowsF + 4;  // row stride of the dS block, floats
+  // The dS block [query][key] sits at columns kStepF .. kStepF + kRowsF - 1 of rows of DSL
+  // floats whose other columns stay zero, so every term of a diagonal sum below is a plain
+  // load (a key outside the block reads +0, which leaves the sum bitwise unchanged).
+  constexpr int DSL = kRowsF + 2 * kStepF;
   constexpr int RING = 256;        // > the 191 diagonals live across two steps
   __shared__ __attribute__((aligned(16))) float Qs[G::TILE];
   __shared__ __attribute__((aligned(16))) float Os[G::TILE];
@@ -409,6 +412,10 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
   zero_tile_pad<DB>(Qs, D);
   zero_tile_pad<DB>(Os, D);
   for (int e = tid; e < RING; e += kThreadsF) ring[e] = 0.f;
+  for (int e = tid; e < kStepF * 2 * kStepF; e += kThreadsF) {  // the zero margins of dsb
+    const int row = e / (2 * kStepF), c = e - row * (2 * kStepF);
+    dsb[row * DSL + (c < kStepF ? c : kRowsF + c)] = 0.f;
+  }
   f32x16 dk[DB], dv[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dk[db] = dv[db] = zero16();
@@ -459,7 +466,7 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
         const float dsv = kvalid ? pv * (ds[r] - Dq[iq]) : 0.f;
         p[r] = pv;
         ds[r] = dsv;
-        dsb[iq * DSL + kk] = dsv;
+        dsb[iq * DSL + kStepF + kk] = dsv;
       }
       dot_positions<DB>(Os, qb * 32, g, l32, p, dv);   // dV^T += dO^T P
       dot_positions<DB>(Qs, qb * 32, g, l32, ds, dk);  // dK^T += Q^T dS
@@ -468,10 +475,9 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
     // Local diagonal x = kk - iq + 63 of this step is partial-row entry R = x - 64 - i0 + S.
     if (tid < kWinF) {
       float acc = 0.f;
-      for (int iq = 0; iq < kStepF; ++iq) {
-        const int c = tid - (kStepF - 1) + iq;
-        if (c >= 0 && c < kRowsF) acc += dsb[iq * DSL + c];
-      }
+      // Column c = tid - 63 + iq of the block is entry kStepF + c of its row, in [1, 254].
+#pragma unroll 16
+      for (int iq = 0; iq < kStepF; ++iq) acc += dsb[iq * DSL + tid + 1 + iq];
       const int R = tid - kStepF - i0 + S;
       if (R >= 0) ring[R & (RING - 1)] += acc;
     }
