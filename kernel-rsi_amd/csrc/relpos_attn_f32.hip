@@ -250,7 +250,10 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int jj = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = j0 + jj < S ? log2_units(fmaf(sc[kb][r], scale, bw[jj - ii + kRowsF - 1])) : -INFINITY;
+        // The window entry (index in [0, kWinF)) is read for every key, so the read does not
+        // wait behind the key test; keys past S then take -inf.
+        const float xv = log2_units(fmaf(sc[kb][r], scale, bw[jj - ii + kRowsF - 1]));
+        const float x = j0 + jj < S ? xv : -INFINITY;
         sc[kb][r] = x;
         mx = fmaxf(mx, x);
       }
@@ -285,8 +288,10 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
 }
 
 // --------------------------------------------------------- backward: delta and dQ
+// At head dims up to 64 the dQ kernel fits two waves per SIMD (256 registers each), which the
+// bound keeps (grids of more than one workgroup per CU then overlap two).
 template <int DB>
-__global__ __launch_bounds__(kThreadsF) void relpos_bwd_dq_f32_kernel(
+__global__ __launch_bounds__(kThreadsF, DB <= 2 ? 2 : 1) void relpos_bwd_dq_f32_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const float* __restrict__ dout, const float* __restrict__ out32, const float* __restrict__ lse,
     float* __restrict__ delta_ws, float* __restrict__ dqkv, int64_t ldd, int S, int H, int D,
@@ -357,8 +362,11 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dq_f32_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int jj = kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        float p = 0.f;
-        if (j0 + jj < S) p = exp2f(log2_units(fmaf(s[r], scale, bw[jj - ii + kRowsF - 1])) - nlse);
+        // Computed for every key (the window read and exp2 do not wait behind the key test;
+        // keys past S have zero K rows and window entries, so the value is finite) and then
+        // dropped past S.
+        const float pv = exp2f(log2_units(fmaf(s[r], scale, bw[jj - ii + kRowsF - 1])) - nlse);
+        const float p = j0 + jj < S ? pv : 0.f;
         s[r] = p * (dp[r] - delta);  // ds
       }
       dot_positions<DB>(Ks, kb * 32, g, l32, s, dq);
@@ -463,7 +471,8 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
         const float pv = exp2f(log2_units(fmaf(p[r], scale, bw[kk - iq + kStepF - 1])) - Lq[iq]);
         // Keys past S have p != 0 (their bias is real) but no gradient: their dK and dV are
         // never stored and their dS is kept out of dpd.
-        const float dsv = kvalid ? pv * (ds[r] - Dq[iq]) : 0.f;
+        const float dd = Dq[iq];  // read for every lane, so it does not wait behind kvalid
+        const float dsv = kvalid ? pv * (ds[r] - dd) : 0.f;
         p[r] = pv;
         ds[r] = dsv;
         dsb[iq * DSL + kStepF + kk] = dsv;
