@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     l_run *= alpha;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(sc[kb][r] - m_new);
+        const float p = __builtin_amdgcn_exp2f(sc[kb][r] - m_new);
         sc[kb][r] = p;
         l_run += p;
       }
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kThreadsF, DB <= 2 ? 2 : 1) void relpos_bwd_dq_f32_
         // Computed for every key (the window read and exp2 do not wait behind the key test;
         // keys past S have zero K rows and window entries, so the value is finite) and then
         // dropped past S.
-        const float pv = exp2f(log2_units(fmaf(s[r], scale, bw[jj - ii + kRowsF - 1])) - nlse);
+        const float pv = __builtin_amdgcn_exp2f(log2_units(fmaf(s[r], scale, bw[jj - ii + kRowsF - 1])) - nlse);
         const float p = j0 + jj < S ? pv : 0.f;
         s[r] = p * (dp[r] - delta);  // ds
       }
@@ -468,7 +468,7 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int iq = qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float pv = exp2f(log2_units(fmaf(p[r], scale, bw[kk - iq + kStepF - 1])) - Lq[iq]);
+        const float pv = __builtin_amdgcn_exp2f(log2_units(fmaf(p[r], scale, bw[kk - iq + kStepF - 1])) - Lq[iq]);
         // Keys past S have p != 0 (their bias is real) but no gradient: their dK and dV are
         // never stored and their dS is kept out of dpd.
         const float dd = Dq[iq];  // read for every lane, so it does not wait behind kvalid
