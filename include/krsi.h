@@ -147,9 +147,10 @@ int krsi_geglu_linear_fwd(const void* x, const void* w, void* out, int64_t rows,
  * Limits: D % 8 == 0 and 8 <= D <= 128, ld_qkv >= 3*H*D, rows of a multiple
  *         of 16 bytes (ld_qkv % 8 == 0 for 16-bit T, % 4 for fp32), S >= 1,
  *         and for 16-bit T S * ld_qkv * 2 < 2^31 bytes (UNSUPPORTED otherwise),
- *         scale finite, and scale == 0 or |scale| * log2(e) >= 2^-60
- *         (BAD_SCALE otherwise: the bias is folded into the score accumulator
- *         as pd * log2(e) / |scale * log2(e)|). Non-causal.                  */
+ *         scale finite, and for 16-bit T scale == 0 or |scale| * log2(e) >=
+ *         2^-60 (BAD_SCALE otherwise: the 16-bit kernels fold the bias into the
+ *         score accumulator as pd * log2(e) / |scale * log2(e)|; the fp32 kernels
+ *         add it directly and take any finite scale). Non-causal.            */
 int krsi_relpos_fwd(const void* qkv, int64_t ld_qkv, const float* pd, void* out, float* out32,
                     float* lse, int32_t B, int32_t S, int32_t H, int32_t D, float scale,
                     int32_t dtype, void* stream);

@@ -42,11 +42,12 @@
 //     entries, staged once per step in 4 copies shifted by one entry, so every
 //     lane reads its 4 consecutive entries with one aligned 128-bit LDS read;
 //     the copy placement puts the 16 lanes of one read phase on distinct banks.
-//   * Online softmax keeps the exact running max per 64-key step (the step
-//     maximum gives p = 1, exact in bf16, as in the reference); the fp32
-//     accumulators are rescaled only when some lane's max moved. The row sum
-//     adds the fp32 p, as the reference; the PV product takes p rounded to the
-//     activation dtype.
+//   * Online softmax keeps a running reference point m per query that trails
+//     the running max by at most kRescaleSlack (2^8 in p): it moves, and the
+//     fp32 accumulators are rescaled, only when a step's max exceeds it by more,
+//     so p <= 2^8 and most steps rescale nothing. l and O are sums relative to m
+//     and lse = m + log2 l is exact for any m. The row sum adds the fp32 p, as
+//     the reference; the PV product takes p rounded to the activation dtype.
 //   * dpd is reduced along the diagonals j - i inside the dK/dV kernel: each
 //     (wave, half-wave) adds its fp32 ds into private LDS rings indexed by
 //     diagonal, two diagonals per 64-bit read-modify-write. Within one
@@ -74,6 +75,10 @@ constexpr int kStep = 64;  // streamed positions per iteration
 // = 0 instead of exp2(-inf - -inf) = NaN; with any finite score the max, and every p, is the
 // same as from -inf (alpha = exp2(-FLT_MAX - m) = 0 = exp2(-inf)).
 constexpr float kMaxStart = -3.40282347e+38f;
+
+// How far (log2 units) a step's max may exceed the forward's running reference point m before
+// m moves and the accumulators are rescaled: p = exp2(s - m) <= 2^8, l <= 2^8 S.
+constexpr float kRescaleSlack = 8.f;
 
 // Compile-time buffer index and tail flag for the unrolled step loops.
 constexpr std::integral_constant<int, 0> kBuf0{};
@@ -360,7 +365,7 @@ __device__ __forceinline__ f32x16 read_bias16(const float* bw, int x0) {
 
 // ------------------------------------------------------------------- forward
 // One 64-key step of the forward for this lane's query: scores (bias folded into
-// the accumulator), exact running max, p = exp2(acc c - m), l += p (fp32, as the
+// the accumulator), running reference point m, p = exp2(acc c - m), l += p (fp32, as the
 // reference's row sum, relpos_attention.py:51), O^T += V^T P^T with P rounded to the
 // activation dtype. TAIL masks keys >= S (last step only).
 template <int DT, int DP, int NW, bool TAIL>
@@ -390,10 +395,12 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[kb][r]);
   mx = xhalf_max(mx) * c;
-  // Exact running max, as the reference (relpos_attention.py:48-50): the step's largest
-  // score maps to p = 1, which bf16 holds exactly. The accumulators are only rescaled when
-  // some lane's max moved.
-  const bool need = mx > m_run;
+  // The reference moves m to the exact running max every step (relpos_attention.py:48-50).
+  // Here m moves only when the step's max exceeds it by more than kRescaleSlack, so p stays
+  // below 2^kRescaleSlack (bf16 and fp16 hold it, rounded relative to its own magnitude as
+  // any p) and the accumulators are rescaled on few steps: at config 5 the exact max moves
+  // in about three steps of four, each rescale ~36 VALU instructions.
+  const bool need = mx > m_run + kRescaleSlack;
   if (__any(need)) {
     const float mnew = need ? mx : m_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - mnew);
@@ -629,8 +636,8 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
 // only group 1's last step can be partial, and it runs in the last iteration. At
 // the end group 1 hands its running max, row sum and accumulators to group 0 through LDS,
 // which merges them: m = max(m0, m1), x = x0 2^(m0 - m) + x1 2^(m1 - m) for l and O. Each
-// half keeps its own exact running max, so p of the second half is rounded relative to that
-// half's maximum rather than to the running maximum over all earlier keys.
+// half keeps its own running reference point, so p of the second half is rounded relative to
+// that half's reference point rather than to one carried over all earlier keys.
 template <int DT, int DP>
 __global__ __launch_bounds__(512, (DP == 64 || DP <= 32 ? 4 : 2)) void relpos_fwd_ks_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
@@ -1361,8 +1368,10 @@ int check_attn(const void* qkv, int64_t ld, int B, int S, int H, int D, float sc
   if (esize == 2 && (int64_t)S * ld * 2 >= ((int64_t)1 << 31)) return KRSI_ERR_UNSUPPORTED;
   if ((ld * esize) % 16 != 0 || !aligned16(qkv)) return KRSI_ERR_MISALIGNED;
   if (!(scale == scale) || scale > 3.0e38f || scale < -3.0e38f) return KRSI_ERR_BAD_SCALE;
+  // Only the 16-bit kernels fold the bias into the score accumulator as pd / c; the fp32
+  // kernels compute q.k * scale + bias directly and take any finite scale.
   const float c = fabsf(scale * kLog2e);
-  if (c != 0.f && c < kMinScaleLog2) return KRSI_ERR_BAD_SCALE;
+  if (esize == 2 && c != 0.f && c < kMinScaleLog2) return KRSI_ERR_BAD_SCALE;
   return KRSI_OK;
 }
 

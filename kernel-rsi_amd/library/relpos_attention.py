@@ -1,9 +1,14 @@
 """Non-causal flash attention with a learned bias indexed by key - query distance, forward and
-backward, on gfx950 (MI355X) HIP kernels: bf16 or fp16 MFMA with fp32 softmax.
+backward, on gfx950 (MI355X) HIP kernels: bf16 or fp16 activations on 16-bit MFMA, fp32
+activations on fp32 MFMA, with the softmax in fp32 either way.
 
 relpos_attention(qkv, pd, B, S, H, D, scale) returns [B*S, H*D].
-  qkv  [B*S, 3*H*D]: the fused projection output, read in place. Token t holds q, k and v of
-       head h at columns h*D, H*D + h*D and 2*H*D + h*D. Any row stride that is a multiple of 8.
+  qkv  [B*S, 3*H*D]: the fused projection output. Token t holds q, k and v of head h at columns
+       h*D, H*D + h*D and 2*H*D + h*D. It is read in place when its rows start on 16-byte
+       boundaries (base address and row stride a multiple of 16 bytes: a row stride that is a
+       multiple of 8 elements for bf16/fp16, of 4 for fp32) with unit column stride. Any other
+       layout is accepted as the reference accepts it, through one contiguous copy of its first
+       3*H*D columns (the gradient still flows to the original tensor).
   pd   [H, 2S-1] fp32: the bias of query i and key j in head h is pd[h, j - i + S - 1]. This
        covers T5 relative positions, ALiBi and any other Toeplitz bias.
 The backward keeps the fp32 output to form delta_i = sum_d dO_id * O_id. It sums dS along its
@@ -46,7 +51,19 @@ class RelPosAttention(torch.autograd.Function):
         return dqkv, dpd, None, None, None, None, None
 
 
+def _kernel_layout(qkv, H, D):
+    """qkv itself when the kernels can read it in place, else a contiguous copy of its q, k and
+    v columns (differentiable, so the gradient of the copy reaches qkv)."""
+    if qkv.dim() != 2:
+        return qkv  # rejected with its shape by the kernel wrapper
+    rows_aligned = qkv.stride(1) == 1 and (qkv.stride(0) * qkv.element_size()) % 16 == 0
+    if rows_aligned and (compiling() or qkv.data_ptr() % 16 == 0):
+        return qkv
+    return qkv[:, :3 * H * D].clone(memory_format=torch.contiguous_format)
+
+
 def relpos_attention(qkv, pd, B, S, H, D, scale):
+    qkv = _kernel_layout(qkv, H, D)
     if compiling():
         return _ops().relpos_fwd_op(qkv, pd, B, S, H, D, scale)[0]
     return RelPosAttention.apply(qkv, pd, B, S, H, D, scale)

@@ -87,6 +87,10 @@ def test_validation_before_launch():
     assert fwd(qkv=FAKE + 2) == E["ALIGN"]
     assert fwd(scale=float("inf")) == E["SCALE"]
     assert fwd(scale=1e-25) == E["SCALE"]    # |scale| log2(e) below 2^-60 (folded bias overflow)
+    # fp32 adds the bias directly, so a tiny scale passes the scale check and the call stops
+    # at the next one (a misaligned out), before any launch.
+    assert lib.krsi_relpos_fwd(FAKE, 384, FAKE, FAKE + 2, FAKE, FAKE, 2, 16, 2, 64, 1e-20, 2, NULL) == E["ALIGN"]
+    assert lib.krsi_relpos_fwd(FAKE, 384, FAKE, FAKE + 2, FAKE, FAKE, 2, 16, 2, 64, 1e-20, 0, NULL) == E["SCALE"]
     assert fwd(S=1 << 20, ld=1024) == E["UNSUP"]  # one (batch, head) slice >= 2^31 bytes
     assert fwd(pd=NULL) == E["NULL"]
     assert fwd(B=40000, H=2) == E["SHAPE"]   # B*H above the grid limit

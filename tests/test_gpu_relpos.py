@@ -138,6 +138,21 @@ def test_relpos_strided_qkv():
     _check(2, 96, 2, 64, 0.125, ref_device="cpu", ld_extra=40)
 
 
+def test_relpos_unaligned_qkv_takes_a_copy():
+    """A qkv view the kernels cannot read in place (base 2 bytes past a 16-byte boundary, odd
+    row stride) runs through one contiguous copy: outputs and gradients equal, bitwise, those of
+    the same values in a contiguous tensor, and the gradient reaches the original view."""
+    log("relpos unaligned qkv B2 S96 H2 D64")
+    B, S, H, D = 2, 96, 2, 64
+    big = seeded((B * S, 3 * H * D + 9), 0)
+    view = big[:, 1:1 + 3 * H * D]
+    assert view.data_ptr() % 16 == 2 and (view.stride(0) * 2) % 16 != 0
+    _, pd, dout = _inputs(B, S, H, D)
+    want = _kernel(view.contiguous(), pd, dout, B, S, H, D, 0.125)
+    got = _kernel(view, pd, dout, B, S, H, D, 0.125)
+    assert all(torch.equal(a, b) for a, b in zip(got, want))
+
+
 def test_relpos_fwd_config4():
     """B2 H16 L1024 D72, scale 1/sqrt(72) (fwd; bwd checked too)."""
     log("relpos config4 B2 S1024 H16 D72")

@@ -3,6 +3,12 @@ caller workspace, called through the C ABI. Its dx and dw must equal, bitwise, t
 krsi_rmsnorm_bwd with a workspace. The check runs on two calls in a row, the second with a
 smaller input (the scratch keeps the first call's partial rows), in each activation dtype,
 and once more after an unrelated workspace call in between."""
+import os
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -69,3 +75,53 @@ def test_noalloc_largest_accepted_and_repeat():
         got = _noalloc(*args)
         torch.cuda.synchronize()
         assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1]), (rows, n)
+
+
+# Run in a fresh process, so that the call inside the capture is the first noalloc call on the
+# device (the one that looks up the device's copy of the scratch array).
+_CAPTURE_SCRIPT = textwrap.dedent("""
+    import sys
+    for p in sys.argv[1:]:
+        sys.path.insert(0, p)
+    import torch
+    import _hip
+    from krsi_testutil import seeded
+    lib = _hip.lib()
+    rows, n = 2048, 4096
+    x = seeded((rows, n), 50)
+    w = seeded((n,), 51, std=0.02, mean=1.0)
+    g = seeded((rows, n), 52)
+    _, rstd = _hip.rmsnorm_fwd(x, w, 1e-6)
+    want_dx, want_dw = _hip.rmsnorm_bwd(g, x, w, rstd)
+    dx, dw = torch.empty_like(x), torch.empty_like(w)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.krsi_rmsnorm_bwd_noalloc(g.data_ptr(), x.data_ptr(), w.data_ptr(), rstd.data_ptr(),
+                                          dx.data_ptr(), dw.data_ptr(), rows, n, 0,
+                                          torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.krsi_error_string(rc)
+    for i in range(2):
+        dx.zero_()
+        dw.zero_()
+        # unrelated work between the replays, a workspace backward of other sizes among it
+        o = seeded((300, 1152), 60 + i)
+        _hip.rmsnorm_bwd(o, o, seeded((1152,), 70, std=0.02, mean=1.0), _hip.rmsnorm_fwd(o, o[0], 1e-6)[1])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dx, want_dx) and torch.equal(dw, want_dw), f"replay {i}"
+    print("noalloc capture ok")
+""")
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """The first noalloc call of a fresh process, made inside torch.cuda.graph capture, then
+    two replays with other work in between: dx and dw equal the workspace entry point's."""
+    log("noalloc rmsnorm bwd: first call inside a graph capture (child process)")
+    here = Path(__file__).resolve().parent
+    root = here.parent
+    paths = [str(here), str(root / "kernel-rsi_amd" / "library"), str(root / "oracle")]
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, *paths], capture_output=True, text=True,
+                       timeout=300, env=dict(os.environ))
+    assert r.returncode == 0 and "noalloc capture ok" in r.stdout, r.stdout + r.stderr
