@@ -535,32 +535,32 @@ def bench_config1(args) -> dict:
 
 
 # ------------------------------------------------------- measured HBM ceiling
-# Read:write byte mix of each bandwidth-bound kernel (algorithmic bytes).
-KERNEL_MIX = {"rmsnorm_fwd": (1, 1), "rmsnorm_bwd": (2, 1), "geglu_fwd": (2, 1), "geglu_bwd": (3, 2)}
+# The row-pattern probe of hw.py that moves each bandwidth-bound kernel's bytes.
+KERNEL_PATTERN = {"rmsnorm_fwd": "rms_fwd", "rmsnorm_bwd": "rms_bwd", "geglu_fwd": "geglu_fwd",
+                  "geglu_bwd": "geglu_bwd"}
 
 
 def attach_stream_ceiling(comps: dict) -> dict:
-    """The cache-cold rate of a plain streaming kernel at each kernel's read:write mix on this
-    box (hw.py's probe). Each bandwidth component gets the ceiling of its fwd+bwd step (the
-    probe's time for the same bytes at the same mixes) and its fraction of it, beside the
-    roofline against the published 8 TB/s."""
+    """The cache-cold rate of each bandwidth-bound kernel's own access pattern with trivial
+    arithmetic on this box (hw.py's row-pattern probes: same arrays, row layout and read:write
+    bytes, best of a sweep over chunks per thread and non-temporal loads and stores). Each
+    bandwidth component gets the ceiling of its fwd+bwd step (the probes' time for the same
+    bytes) and its fraction of it, beside the roofline against the published 8 TB/s."""
     import hw
-    wanted = sorted({KERNEL_MIX[k] for c in comps.values() for k in c.get("kernels", {}) if k in KERNEL_MIX})
-    if not wanted:
+    if not any(k in KERNEL_PATTERN for c in comps.values() for k in c.get("kernels", {})):
         return {}
-    probe = hw.probe_stream(hw.Clock(samples=3), quick=True, mixes=wanted)
+    probe = hw.probe_patterns(hw.Clock(samples=3), quick=True)
     if "error" in probe:
         return probe
-    gbs = {mix: probe[f"r{mix[0]}w{mix[1]}"]["gbs"] for mix in wanted}
     for comp in comps.values():
-        ks = {k: v for k, v in comp.get("kernels", {}).items() if k in KERNEL_MIX}
+        ks = {k: v for k, v in comp.get("kernels", {}).items() if k in KERNEL_PATTERN}
         if not ks:
             continue
-        t = sum(v["bytes"] / (gbs[KERNEL_MIX[k]] * 1e9) for k, v in ks.items())
+        t = sum(v["bytes"] / (probe[KERNEL_PATTERN[k]]["gbs"] * 1e9) for k, v in ks.items())
         ceil = sum(v["bytes"] for v in ks.values()) / t / 1e9
         comp["stream_ceiling"] = {"GB/s": round(ceil, 1), "frac": round(comp["value"] / ceil, 4),
-                                  "source": "hw.py streaming probe at each kernel's read:write mix, this run"}
-    return {f"stream_r{r}w{w}_GB/s": v for (r, w), v in gbs.items()}
+                                  "source": "hw.py row-pattern probes of each kernel's traffic, this run"}
+    return {f"pattern_{k}_GB/s": v["gbs"] for k, v in probe.items()}
 
 
 def attach_gemm_ceiling(comps: dict) -> dict:

@@ -62,7 +62,8 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(const typename Elem<DT>:
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     const int c = gtid + k * GT;
-    xv[k] = (live && c < nch) ? xr[c] : u32x4{0u, 0u, 0u, 0u};
+    // x streams in non-temporally (cache-cold at config 2: forward 88.0 -> 87.1 us).
+    xv[k] = (live && c < nch) ? __builtin_nontemporal_load(&xr[c]) : u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {

@@ -10,6 +10,8 @@ package's roofline discussion uses:
   * the published peaks;
   * the rate of a hand-written streaming kernel at each read:write mix (libkrsi_probe.so), the
     practical HBM ceiling for bandwidth-bound kernels, which torch's copy does not reach;
+  * the rate of each bandwidth-bound kernel's own access pattern with trivial arithmetic
+    (the row-pattern probes of libkrsi_probe.so), the ceiling that kernel is measured against;
   * launch costs;
   * the ridge points.
 The probes are a table of small functions. Each runs under `Clock`, which reports the median
@@ -174,6 +176,64 @@ def probe_stream(clock: Clock, quick: bool = False, mixes=STREAM_MIXES) -> dict:
     return res
 
 
+# The library's bandwidth-bound kernels at their BASELINE shapes: (pattern, rows, chunks of 16
+# bytes in the narrow row, bytes per call, rotating sets).
+PATTERNS = {
+    "rms_fwd": (0, 32768, 512, 32768 * 512 * 16 * 2, 4),
+    "rms_bwd": (1, 32768, 512, 32768 * 512 * 16 * 3, 4),
+    "geglu_fwd": (2, 8192, 512, 8192 * 512 * 16 * 3, 6),
+    "geglu_bwd": (3, 8192, 512, 8192 * 512 * 16 * 5, 6),
+}
+
+
+def probe_patterns(clock: Clock, quick: bool = False) -> dict:
+    """GB/s of the row-pattern probes (libkrsi_probe.so krsi_probe_rows): each bandwidth-bound
+    kernel's exact HBM traffic (same arrays, row layout and read:write bytes) with trivial
+    arithmetic, best over chunks per thread, rows per workgroup and non-temporal loads / stores.
+    Cache-cold: sets of arrays rotate, several hundred MB each, past the 256 MB MALL."""
+    import ctypes
+
+    path = HERE / "libkrsi_probe.so"
+    if not path.is_file():
+        return {"error": f"{path.name} not built"}
+    lib = ctypes.CDLL(str(path))
+    lib.krsi_probe_rows.restype = ctypes.c_int
+    lib.krsi_probe_rows.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                                        ctypes.c_int, ctypes.c_void_p]
+    stream = torch.cuda.current_stream().cuda_stream
+    shapes = ((1, 1), (2, 1), (4, 1), (1, 2), (2, 2), (1, 4))
+    if quick:
+        shapes = ((1, 1), (2, 1))
+    res = {}
+    for name, (pat, rows, n, nbytes, nsets) in PATTERNS.items():
+        chunk = rows * n * 16
+        sizes = {0: ([chunk], [chunk]), 1: ([chunk, chunk], [chunk]), 2: ([2 * chunk], [chunk]),
+                 3: ([chunk, 2 * chunk], [2 * chunk])}[pat]
+        sets = [([torch.empty(b, dtype=torch.uint8, device="cuda").random_(0, 256) for b in sizes[0]],
+                 [torch.empty(b, dtype=torch.uint8, device="cuda") for b in sizes[1]]) for _ in range(nsets)]
+        ins = [(ctypes.c_void_p * 2)(*([t.data_ptr() for t in i] + [0] * (2 - len(i)))) for i, _ in sets]
+        outs = [(ctypes.c_void_p * 1)(o[0].data_ptr()) for _, o in sets]
+        best = (0.0, None)
+        for vpt, rpb in shapes:
+            for ntl in (0, 1):
+                for nts in (0, 1):
+                    k = [0]
+
+                    def call():
+                        i = k[0] % nsets
+                        k[0] += 1
+                        rc = lib.krsi_probe_rows(pat, vpt, rpb, ntl, nts, ins[i], outs[i], rows, n, stream)
+                        if rc:
+                            raise RuntimeError(f"krsi_probe_rows({pat}, {vpt}, {rpb}, {ntl}, {nts}) returned {rc}")
+                    gbs = nbytes / clock.ms(call, 2 * nsets) / 1e6
+                    if gbs > best[0]:
+                        best = (gbs, {"vpt": vpt, "rows_per_block": rpb, "nt_load": ntl, "nt_store": nts})
+        res[name] = {"gbs": round(best[0]), **best[1]}
+        del sets, ins, outs
+        torch.cuda.empty_cache()
+    return res
+
+
 def probe_launch(clock: Clock) -> dict:
     """Microseconds per tiny kernel: one stream launch of a torch op, one graph replay."""
     x = torch.zeros(1, device="cuda")
@@ -202,6 +262,7 @@ def collect(quick: bool = False) -> dict:
            "memory_gb": round(props.total_memory / 2 ** 30, 1), "tflops": tflops}
     rec.update(probe_bandwidth(clock))
     rec["stream_kernel_gbs"] = probe_stream(clock, quick)
+    rec["pattern_probe_gbs"] = probe_patterns(clock, quick)
     stream_bw = max(rec["bw_copy_gbs"], rec["bw_read_gbs"])
     rec["ridge_flop_per_byte"] = {k: round(v * 1e3 / stream_bw, 1) for k, v in tflops.items()
                                   if isinstance(v, (int, float))}
@@ -238,6 +299,8 @@ def main(argv=None) -> int:
     if args.stream_only:
         for mix, v in probe_stream(Clock(samples=5), args.quick).items():
             print(f"{mix}: {v}", flush=True)
+        for name, v in probe_patterns(Clock(samples=5), args.quick).items():
+            print(f"{name}: {v}", flush=True)
         return 0
     rec = collect(args.quick)
     width = max(map(len, rec))

@@ -76,6 +76,98 @@ int launch(int unroll, int nt, int blocks, const void* const* in, void* const* o
   return 1;
 }
 
+// Row-pattern probes: the exact HBM traffic of each bandwidth-bound kernel of the library with
+// trivial arithmetic, so a kernel that matches its pattern's best rate is at what the memory
+// system gives that access pattern. n = 16-byte chunks of the narrow row (the output row of
+// the GEGLU forward, the input row of everything else):
+//   PAT 0 RMSNorm forward   in0 [rows, n]                 -> out0 [rows, n]
+//   PAT 1 RMSNorm backward  in0, in1 [rows, n]            -> out0 [rows, n]
+//   PAT 2 GEGLU forward     in0 [rows, 2n] (a | b halves) -> out0 [rows, n]
+//   PAT 3 GEGLU backward    in0 [rows, n], in1 [rows, 2n] -> out0 [rows, 2n]
+// A workgroup of 256 threads covers 256 VPT chunks of RPB consecutive rows (grid: column tiles
+// x row blocks, the row blocks strided past 65535); every thread issues all of its loads before
+// its first store. NTL / NTS: non-temporal loads / stores. Every index stays below its array's
+// size: chunk c < n is checked and rows < rows.
+template <bool NT>
+__device__ __forceinline__ u32x4 get(const u32x4* p) {
+  if (NT) return __builtin_nontemporal_load(p);
+  return *p;
+}
+
+template <int PAT, int VPT, int RPB, bool NTL, bool NTS>
+__global__ __launch_bounds__(256) void rows_kernel(const u32x4* __restrict__ in0, const u32x4* __restrict__ in1,
+                                                   u32x4* __restrict__ out0, int64_t rows, int n) {
+  constexpr int NL = (PAT == 0) ? 1 : 2;  // loads per chunk of the narrow row
+  constexpr int NS = (PAT == 3) ? 2 : 1;  // stores per chunk
+  for (int64_t rb = (int64_t)blockIdx.y * RPB; rb < rows; rb += (int64_t)gridDim.y * RPB) {
+    u32x4 v[RPB][VPT][NL];
+#pragma unroll
+    for (int i = 0; i < RPB; ++i)
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int64_t r = rb + i < rows ? rb + i : rows - 1;
+        int c = blockIdx.x * 256 * VPT + k * 256 + threadIdx.x;
+        c = c < n ? c : n - 1;
+        if (PAT == 0) v[i][k][0] = get<NTL>(in0 + r * n + c);
+        if (PAT == 1) {
+          v[i][k][0] = get<NTL>(in0 + r * n + c);
+          v[i][k][1] = get<NTL>(in1 + r * n + c);
+        }
+        if (PAT == 2) {
+          v[i][k][0] = get<NTL>(in0 + r * 2 * n + c);
+          v[i][k][1] = get<NTL>(in0 + r * 2 * n + n + c);
+        }
+        if (PAT == 3) {
+          v[i][k][0] = get<NTL>(in0 + r * n + c) + get<NTL>(in1 + r * 2 * n + c);
+          v[i][k][1] = get<NTL>(in1 + r * 2 * n + n + c);
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < RPB; ++i)
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int64_t r = rb + i;
+        const int c = blockIdx.x * 256 * VPT + k * 256 + threadIdx.x;
+        if (r >= rows || c >= n) continue;
+        const u32x4 a = NL == 2 ? v[i][k][0] + v[i][k][1] : v[i][k][0] + 1u;
+        if (NS == 1) put<NTS>(out0 + r * n + c, a);
+        else {
+          put<NTS>(out0 + r * 2 * n + c, a);
+          put<NTS>(out0 + r * 2 * n + n + c, v[i][k][1] ^ a);
+        }
+      }
+  }
+}
+
+template <int PAT, int VPT, int RPB>
+int launch_rows(int ntl, int nts, const void* const* in, void* const* out, int64_t rows, int n, hipStream_t st) {
+  const u32x4* a0 = (const u32x4*)in[0];
+  const u32x4* a1 = PAT == 0 ? nullptr : (const u32x4*)in[1];
+  u32x4* o0 = (u32x4*)out[0];
+  const int64_t ry = (rows + RPB - 1) / RPB;
+  const dim3 grid((unsigned)((n + 256 * VPT - 1) / (256 * VPT)), (unsigned)(ry < 65535 ? ry : 65535));
+#define KRSI_ROWS_CASE(L, S)                                                                                   \
+  if (ntl == L && nts == S) {                                                                                  \
+    hipLaunchKernelGGL((rows_kernel<PAT, VPT, RPB, L, S>), grid, dim3(256), 0, st, a0, a1, o0, rows, n);        \
+    return hipGetLastError() == hipSuccess ? 0 : 2;                                                            \
+  }
+  KRSI_ROWS_CASE(false, false) KRSI_ROWS_CASE(false, true) KRSI_ROWS_CASE(true, false) KRSI_ROWS_CASE(true, true)
+#undef KRSI_ROWS_CASE
+  return 1;
+}
+
+template <int PAT>
+int launch_rows_pat(int vpt, int rpb, int ntl, int nts, const void* const* in, void* const* out, int64_t rows,
+                    int n, hipStream_t st) {
+  if (vpt == 1 && rpb == 1) return launch_rows<PAT, 1, 1>(ntl, nts, in, out, rows, n, st);
+  if (vpt == 2 && rpb == 1) return launch_rows<PAT, 2, 1>(ntl, nts, in, out, rows, n, st);
+  if (vpt == 4 && rpb == 1) return launch_rows<PAT, 4, 1>(ntl, nts, in, out, rows, n, st);
+  if (vpt == 1 && rpb == 2) return launch_rows<PAT, 1, 2>(ntl, nts, in, out, rows, n, st);
+  if (vpt == 2 && rpb == 2) return launch_rows<PAT, 2, 2>(ntl, nts, in, out, rows, n, st);
+  if (vpt == 1 && rpb == 4) return launch_rows<PAT, 1, 4>(ntl, nts, in, out, rows, n, st);
+  return 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -111,6 +203,23 @@ int krsi_probe_stream(int reads, int writes, int unroll, int nontemporal, int bl
     return 1;
   }
   return 1;
+}
+
+// Row-pattern probe (rows_kernel above): pattern 0..3, vpt in {1, 2, 4} with rpb 1, vpt in
+// {1, 2} with rpb 2, or vpt 1 with rpb 4; ntl / nts 0 or 1. in[0..1] and out[0] sized for the
+// pattern. Returns 0, 1 for an unsupported combination (nothing launched), 2 if the launch
+// was rejected.
+int krsi_probe_rows(int pattern, int vpt, int rpb, int ntl, int nts, const void* const* in, void* const* out,
+                    int64_t rows, int n, void* stream) {
+  if (rows <= 0 || n <= 0 || !in || !out) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (pattern) {
+    case 0: return launch_rows_pat<0>(vpt, rpb, ntl, nts, in, out, rows, n, st);
+    case 1: return launch_rows_pat<1>(vpt, rpb, ntl, nts, in, out, rows, n, st);
+    case 2: return launch_rows_pat<2>(vpt, rpb, ntl, nts, in, out, rows, n, st);
+    case 3: return launch_rows_pat<3>(vpt, rpb, ntl, nts, in, out, rows, n, st);
+    default: return 1;
+  }
 }
 
 }  // extern "C"
