@@ -70,6 +70,8 @@ namespace {
 
 constexpr int kStep = 64;  // streamed positions per iteration
 
+constexpr int align_up(int x, int a) { return (x + a - 1) / a * a; }
+
 // Start of the running max: the most negative finite float rather than -inf. A step whose
 // scores are all -inf (keys masked by -inf entries of the bias table) then gives p = exp2(-inf)
 // = 0 instead of exp2(-inf - -inf) = NaN; with any finite score the max, and every p, is the
@@ -821,9 +823,22 @@ __device__ __forceinline__ void dq_step(const uint16_t* Ks, const uint16_t* Vs, 
   }
 }
 
-template <int DT, int DP, int NW>
-__global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
-    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+// LDS of the dQ kernel: the K tiles, then the V tiles (one array, so the dQ staging can reuse
+// all of it), then the bias windows; each region 256-byte aligned.
+template <int DP, int NW>
+struct DqLds {
+  static constexpr int TILE = kStep * Geo<DP>::DPV;
+  static constexpr int KV_BYTES = 4 * TILE * 2;
+  static constexpr int BW_OFF = align_up(KV_BYTES, 256);
+  static constexpr int BYTES = BW_OFF + 2 * 4 * Blk<NW>::WLD * 4;
+};
+
+// The dQ kernel's work for query block `tile` (of the grid's B H ceil(S / 128)), with its LDS
+// at `lds` (DqLds). DELTA_GIVEN: delta is read from delta_ws (written by relpos_delta_kernel)
+// rather than formed from dO and O32 and written there.
+template <int DT, int DP, int NW, bool DELTA_GIVEN>
+__device__ __forceinline__ void bwd_dq_body(
+    int tile, unsigned char* lds, const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ out32,
     const float* __restrict__ lse, float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv,
     int64_t ldd, int S, int H, int D, Fold f, float scale) {
@@ -831,9 +846,8 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   using K = Blk<NW>;
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
-  // K tiles, then V tiles (one array, so the dQ staging can reuse all of it).
-  __shared__ __attribute__((aligned(16))) uint16_t KVs[4 * TILE];
-  __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
+  uint16_t* const KVs = reinterpret_cast<uint16_t*>(lds);
+  float* const Bw = reinterpret_cast<float*>(lds + DqLds<DP, NW>::BW_OFF);
   uint16_t* const Ks = KVs;
   uint16_t* const Vs = KVs + 2 * TILE;
 
@@ -841,7 +855,6 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
   TileLane<DP> L;
   L.init(lane);
   const int nqb = (S + K::ROWS - 1) / K::ROWS;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
   const int bh = tile / nqb, b = bh / H, h = bh - b * H;
   const int qb = tile - bh * nqb;
   const int i_wg = qb * K::ROWS;
@@ -869,22 +882,24 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
     const uint32_t m = lane_mask(ok);
     qreg[s] = masked(fold_operand(ld16(ok ? q0 + (int64_t)qi * ld + d0 : q0), f), m);
     doreg[s] = ld16_masked(dout + obase + d0, dout, ok, m);
-    const f32x4 o0 = ld16f_masked(out32 + obase + d0, out32, ok, m);
-    const f32x4 o1 = ld16f_masked(out32 + obase + d0 + 4, out32, ok, m);
-    float df[8];
-    Elem<DT>::unpack(doreg[s], df);
+    if constexpr (!DELTA_GIVEN) {
+      const f32x4 o0 = ld16f_masked(out32 + obase + d0, out32, ok, m);
+      const f32x4 o1 = ld16f_masked(out32 + obase + d0 + 4, out32, ok, m);
+      float df[8];
+      Elem<DT>::unpack(doreg[s], df);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dsum += df[e] * o0[e];
+      for (int e = 0; e < 4; ++e) dsum += df[e] * o0[e];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dsum += df[4 + e] * o1[e];
+      for (int e = 0; e < 4; ++e) dsum += df[4 + e] * o1[e];
+    }
   }
-  const float delta = xhalf_sum(dsum);
+  const float delta = DELTA_GIVEN ? (qvalid ? delta_ws[(int64_t)bh * S + qi] : 0.f) : xhalf_sum(dsum);
   f32x16 negd;
 #pragma unroll
   for (int r = 0; r < 16; ++r) negd[r] = -delta;
   // -inf makes p = exp2(acc c - lse) exactly 0 on lanes past S (their acc is finite).
   const float neg_lse = qvalid ? -lse[(int64_t)bh * S + qi] : -INFINITY;
-  if (qvalid && g == 0) delta_ws[(int64_t)bh * S + qi] = delta;
+  if (!DELTA_GIVEN && qvalid && g == 0) delta_ws[(int64_t)bh * S + qi] = delta;
 
   f32x16 dq[G::DB];
 #pragma unroll
@@ -931,7 +946,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
       step(t, kBuf0, kTail);
   }
 
-  if constexpr (NW * kWaveTile * 4 <= (int)sizeof(KVs)) {
+  if constexpr (NW * kWaveTile * 4 <= DqLds<DP, NW>::KV_BYTES) {
     __syncthreads();  // every wave is done with the last tiles
     store_rows_staged<DT, DP, false>(dq, [scale](float x) { return x * scale; }, lane,
                                      min(32, S - (i_wg + wave * 32)), (tok0 + i_wg + wave * 32) * ldd + (int64_t)h * D,
@@ -951,6 +966,17 @@ __global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_ker
         }
       }
   }
+}
+
+template <int DT, int DP, int NW>
+__global__ __launch_bounds__(64 * NW, (DP <= 96 ? 2 : 1)) void relpos_bwd_dq_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    const uint16_t* __restrict__ dout, const float* __restrict__ out32,
+    const float* __restrict__ lse, float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv,
+    int64_t ldd, int S, int H, int D, Fold f, float scale) {
+  __shared__ __attribute__((aligned(256))) unsigned char lds[DqLds<DP, NW>::BYTES];
+  bwd_dq_body<DT, DP, NW, false>(xcd_tile(blockIdx.x, gridDim.x), lds, qkv, ld, pd, dout, out32, lse, delta_ws,
+                                 dqkv, ldd, S, H, D, f, scale);
 }
 
 // ---------------------------------------------------------- backward: dK, dV, dpd
@@ -1043,32 +1069,50 @@ __device__ __forceinline__ float ring_fold(float* ring, int r, int off1) {
   for (int e = 0; e < 8; ++e) v += x[e];
   return quad_sum(v);
 }
+// LDS of the dK/dV kernel, each region 256-byte aligned: the dpd rings, a sink for the ds of
+// keys past S, the Q and dO tiles, the step's -lse and -delta windows, the bias windows.
+template <int DP, int NW>
+struct DkdvLds {
+  static constexpr int TILE = kStep * Geo<DP>::DPV;
+  static constexpr int RINGF = 2 * 2 * NW * kRingSlots;
+  static constexpr int RING_OFF = 0;
+  static constexpr int SINK_OFF = align_up(RING_OFF + RINGF * 4, 256);
+  static constexpr int QS_OFF = align_up(SINK_OFF + 320 * 4, 256);
+  static constexpr int TILES_BYTES = 2 * TILE * 2;  // one double-buffered tile array
+  static constexpr int OS_OFF = align_up(QS_OFF + TILES_BYTES, 256);
+  static constexpr int LQ_OFF = align_up(OS_OFF + TILES_BYTES, 256);
+  static constexpr int DQ_OFF = align_up(LQ_OFF + 2 * kStep * 4, 256);
+  static constexpr int BW_OFF = align_up(DQ_OFF + 2 * kStep * 4, 256);
+  static constexpr int BYTES = BW_OFF + 2 * 4 * Blk<NW>::WLD * 4;
+};
+
+// The dK/dV kernel's work for key block `tile`, with its LDS at `lds` (DkdvLds).
 template <int DT, int DP, int NW>
-__global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
-    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+__device__ __forceinline__ void bwd_dkdv_body(
+    int tile, unsigned char* lds, const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd,
     float* __restrict__ part, int S, int H, int D, Fold f, float scale) {
   using G = Geo<DP>;
   using K = Blk<NW>;
+  using LY = DkdvLds<DP, NW>;
   static_assert(K::ROWS <= 128, "the dpd rings hold 256 live diagonals");
   static_assert(K::NT == 256, "the ring fold maps 4 lanes to each of 64 diagonals");
   constexpr int TILE = kStep * G::DPV;
   constexpr int BWIN = 4 * K::WLD;
-  constexpr int RINGF = 2 * 2 * NW * kRingSlots;
-  __shared__ __attribute__((aligned(16))) float ring[RINGF];
-  __shared__ __attribute__((aligned(16))) float sink[320];  // ds of keys past S
-  __shared__ __attribute__((aligned(16))) uint16_t Qs[2 * TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t Os[2 * TILE];
-  __shared__ __attribute__((aligned(16))) float Lq[2 * kStep];
-  __shared__ __attribute__((aligned(16))) float Dq[2 * kStep];
-  __shared__ __attribute__((aligned(16))) float Bw[2 * BWIN];
+  constexpr int RINGF = LY::RINGF;
+  float* const ring = reinterpret_cast<float*>(lds + LY::RING_OFF);
+  float* const sink = reinterpret_cast<float*>(lds + LY::SINK_OFF);
+  uint16_t* const Qs = reinterpret_cast<uint16_t*>(lds + LY::QS_OFF);
+  uint16_t* const Os = reinterpret_cast<uint16_t*>(lds + LY::OS_OFF);
+  float* const Lq = reinterpret_cast<float*>(lds + LY::LQ_OFF);
+  float* const Dq = reinterpret_cast<float*>(lds + LY::DQ_OFF);
+  float* const Bw = reinterpret_cast<float*>(lds + LY::BW_OFF);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
   L.init(lane);
   const int nkb = (S + K::ROWS - 1) / K::ROWS;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
   const int bh = tile / nkb, b = bh / H, h = bh - b * H;
   const int kblk = tile - bh * nkb;
   const int j_wg = kblk * K::ROWS;
@@ -1241,7 +1285,7 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 
   // D layout: lane = head dim d (n), register r = tile row 8(r/4) + 4g + r%4, which holds
   // key kperm(row) of this wave.
-  if constexpr (2 * kColTile * 4 <= (int)sizeof(Qs)) {
+  if constexpr (2 * kColTile * 4 <= LY::TILES_BYTES) {
     // Staged: waves 0-1 in the Q tiles, 2-3 in the dO tiles (free since the fold's barrier).
     float* wt = reinterpret_cast<float*>(wave < 2 ? Qs : Os) + (wave & 1) * kColTile;
     const int nrows = min(32, S - (j_wg + wave * 32));
@@ -1265,6 +1309,68 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
       }
     }
   }
+}
+
+template <int DT, int DP, int NW>
+__global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd,
+    float* __restrict__ part, int S, int H, int D, Fold f, float scale) {
+  __shared__ __attribute__((aligned(256))) unsigned char lds[DkdvLds<DP, NW>::BYTES];
+  bwd_dkdv_body<DT, DP, NW>(xcd_tile(blockIdx.x, gridDim.x), lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd,
+                            part, S, H, D, f, scale);
+}
+
+// --------------------------------------------- backward on small grids: one launch for both
+// delta[bh, i] = sum_d dO[i, d] O32[i, d] for one (query, head) per thread, summed exactly as the
+// dQ kernel's prologue sums it (the lower half-wave's 8-element chunks 16s..16s+7, the upper
+// half's 16s+8..16s+15, each in order, then lower + upper), so delta is bitwise the same.
+template <int DT>
+__global__ __launch_bounds__(256) void relpos_delta_kernel(const uint16_t* __restrict__ dout,
+                                                           const float* __restrict__ out32,
+                                                           float* __restrict__ delta_ws, int B, int S, int H,
+                                                           int D) {
+  const int64_t n = (int64_t)B * H * S;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int64_t bh = e / S, i = e - bh * S;
+  const int64_t b = bh / H, h = bh - b * H;
+  const int64_t base = (b * S + i) * H * D + h * D;
+  float half[2] = {0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+    for (int d0 = 8 * g; d0 < D; d0 += 16) {
+      float df[8];
+      Elem<DT>::unpack(ld16(dout + base + d0), df);
+      const f32x4 o0 = *reinterpret_cast<const f32x4*>(out32 + base + d0);
+      const f32x4 o1 = *reinterpret_cast<const f32x4*>(out32 + base + d0 + 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) half[g] += df[q] * o0[q];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) half[g] += df[4 + q] * o1[q];
+    }
+  delta_ws[e] = half[0] + half[1];
+}
+
+// The dQ and dK/dV kernels in one grid, for grids too small to give every CU two workgroups
+// of either alone (at most 256 workgroups each): workgroup c of the XCD-ordered grid takes dQ
+// block c / 2 (c even) or dK/dV block c / 2 (c odd), so two workgroups share each CU and the
+// two kinds of the same (batch, head) share an XCD's L2. delta comes from relpos_delta_kernel.
+template <int DT, int DP>
+__global__ __launch_bounds__(256, (DP <= 64 ? 2 : 1)) void relpos_bwd_pair_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
+    const uint16_t* __restrict__ dout, const float* __restrict__ out32, const float* __restrict__ lse,
+    float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd, float* __restrict__ part, int S, int H,
+    int D, Fold f, float scale) {
+  constexpr int BYTES = DqLds<DP, 4>::BYTES > DkdvLds<DP, 4>::BYTES ? DqLds<DP, 4>::BYTES : DkdvLds<DP, 4>::BYTES;
+  __shared__ __attribute__((aligned(256))) unsigned char lds[BYTES];
+  const int c = xcd_tile(blockIdx.x, gridDim.x);
+  if (c & 1)
+    bwd_dkdv_body<DT, DP, 4>(c >> 1, lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd, part, S, H, D, f, scale);
+  else
+    bwd_dq_body<DT, DP, 4, true>(c >> 1, lds, qkv, ld, pd, dout, out32, lse, delta_ws, dqkv, ldd, S, H, D, f,
+                                 scale);
 }
 
 // dpd[h, k] = sum over b and key blocks of the partial rows (row of key block kb holds
@@ -1358,6 +1464,13 @@ constexpr int kFwdNW = 4;
 constexpr unsigned kFwdSplitBelow = 512;
 constexpr int kDqNW = 4;
 constexpr int kDkdvNW = 4;
+// Backward grids of at most this many workgroups per kernel (half the MI355X's 256 CUs) run the
+// dQ and dK/dV work in one launch (relpos_bwd_pair_kernel), at head dims up to 64, where the
+// dK/dV kernel's LDS and registers leave room for two workgroups per CU. A/B, backward, builds
+// interleaved in one process: B1 S300 H16 D64 (48 workgroups each) 27.1 -> 23.6 us, B1 S130 H8
+// D64 (16) 21.3 -> 19.0 us; at 256 each it was slower (B4 S512 H16 D64 40.1 -> 42.4 us, B2
+// S1024 H16 D64 61.4 -> 63.8 us), so larger grids keep the two launches.
+constexpr int kPairBwdMax = 128;
 
 // Smallest nonzero |scale| * log2(e) the folded bias accepts: pd * log2(e) / c must
 // stay finite for any realistic table.
@@ -1423,6 +1536,17 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_delta_bytes(B, S, H));
   const int nqb = (int)ceil_div(S, KQ::ROWS);
   const int nkb = (int)ceil_div(S, KK::ROWS);
+  static_assert(KQ::ROWS == KK::ROWS && kDqNW == 4 && kDkdvNW == 4, "the pair kernel pairs equal grids");
+  if (DP <= 64 && nqb * B * H <= kPairBwdMax) {  // larger head dims: 1 workgroup of either per CU
+    const int64_t n = (int64_t)B * H * S;
+    hipLaunchKernelGGL((relpos_delta_kernel<DT>), dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st,
+                       (const uint16_t*)dout, out32, delta, B, S, H, D);
+    hipLaunchKernelGGL((relpos_bwd_pair_kernel<DT, DP>), dim3((unsigned)(2 * nqb * B * H)), dim3(256), 0, st,
+                       (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32, lse, delta, (uint16_t*)dqkv,
+                       ldd, part, S, H, D, f, scale);
+    launch_dpd_reduce(part, dpd, B, S, H, st);
+    return;
+  }
   hipLaunchKernelGGL((relpos_bwd_dq_kernel<DT, DP, kDqNW>), dim3((unsigned)(nqb * B * H)),
                      dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
                      lse, delta, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
