@@ -1354,9 +1354,9 @@ __global__ __launch_bounds__(256) void relpos_delta_kernel(const uint16_t* __res
 }
 
 // The dQ and dK/dV kernels in one grid, for grids too small to give every CU two workgroups
-// of either alone (at most 256 workgroups each): workgroup c of the XCD-ordered grid takes dQ
-// block c / 2 (c even) or dK/dV block c / 2 (c odd), so two workgroups share each CU and the
-// two kinds of the same (batch, head) share an XCD's L2. delta comes from relpos_delta_kernel.
+// of either alone (at most 256 workgroups each): half the workgroups take dQ blocks and half
+// dK/dV blocks, so the two kinds run side by side on each CU, and the two kinds of the same
+// (batch, head) share an XCD's L2. delta comes from relpos_delta_kernel.
 template <int DT, int DP>
 __global__ __launch_bounds__(256, (DP <= 64 ? 2 : 1)) void relpos_bwd_pair_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
@@ -1365,11 +1365,22 @@ __global__ __launch_bounds__(256, (DP <= 64 ? 2 : 1)) void relpos_bwd_pair_kerne
     int D, Fold f, float scale) {
   constexpr int BYTES = DqLds<DP, 4>::BYTES > DkdvLds<DP, 4>::BYTES ? DqLds<DP, 4>::BYTES : DkdvLds<DP, 4>::BYTES;
   __shared__ __attribute__((aligned(256))) unsigned char lds[BYTES];
+  // XCD x holds tiles [x q, (x + 1) q) of the XCD-ordered grid and its 32 CUs take them in
+  // order, one per CU before any takes a second: with q even the first half of an XCD's range
+  // runs dQ blocks and the second half the dK/dV blocks of the same (batch, head)s, so a CU
+  // holding two workgroups holds one of each. Otherwise the kinds alternate.
   const int c = xcd_tile(blockIdx.x, gridDim.x);
-  if (c & 1)
-    bwd_dkdv_body<DT, DP, 4>(c >> 1, lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd, part, S, H, D, f, scale);
+  const int N = gridDim.x;
+  int kind = c & 1, idx = c >> 1;
+  if (N % (2 * kXcds) == 0) {
+    const int q = N / kXcds, half = q / 2, x = c / q, k = c - x * q;
+    kind = k >= half;
+    idx = x * half + k - kind * half;
+  }
+  if (kind)
+    bwd_dkdv_body<DT, DP, 4>(idx, lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd, part, S, H, D, f, scale);
   else
-    bwd_dq_body<DT, DP, 4, true>(c >> 1, lds, qkv, ld, pd, dout, out32, lse, delta_ws, dqkv, ldd, S, H, D, f,
+    bwd_dq_body<DT, DP, 4, true>(idx, lds, qkv, ld, pd, dout, out32, lse, delta_ws, dqkv, ldd, S, H, D, f,
                                  scale);
 }
 
@@ -1464,13 +1475,16 @@ constexpr int kFwdNW = 4;
 constexpr unsigned kFwdSplitBelow = 512;
 constexpr int kDqNW = 4;
 constexpr int kDkdvNW = 4;
-// Backward grids of at most this many workgroups per kernel (half the MI355X's 256 CUs) run the
-// dQ and dK/dV work in one launch (relpos_bwd_pair_kernel), at head dims up to 64, where the
-// dK/dV kernel's LDS and registers leave room for two workgroups per CU. A/B, backward, builds
-// interleaved in one process: B1 S300 H16 D64 (48 workgroups each) 27.1 -> 23.6 us, B1 S130 H8
-// D64 (16) 21.3 -> 19.0 us; at 256 each it was slower (B4 S512 H16 D64 40.1 -> 42.4 us, B2
-// S1024 H16 D64 61.4 -> 63.8 us), so larger grids keep the two launches.
-constexpr int kPairBwdMax = 128;
+// Backward grids of at most this many workgroups per kernel (the MI355X's 256 CUs) run the dQ
+// and dK/dV work in one launch (relpos_bwd_pair_kernel), at head dims up to 64, where the
+// dK/dV kernel's LDS and registers leave room for two workgroups per CU. Above 128 per kernel
+// the grid must split evenly over the 8 XCDs in halves (2n % 16 == 0), so that the two
+// workgroups a CU holds are one of each kind. A/B, backward, builds interleaved in one
+// process: B1 S300 H16 D64 (48 workgroups each) 27.1 -> 23.6 us, B1 S130 H8 D64 (16) 21.3 ->
+// 19.0 us, B2 S1024 H16 D64 (256) 59.5 -> 56.3 us, B1 S2048 H16 D64 (256) 98.0 -> 92.3 us,
+// B4 S512 H16 D64 (256) 39.9 -> 40.0 us; pairing by parity of the tile instead put two of the
+// same kind on each CU and lost at 256 (B2 S1024 H16 D64 59.5 -> 61.2 us).
+constexpr int kPairBwdMax = 256;
 
 // Smallest nonzero |scale| * log2(e) the folded bias accepts: pd * log2(e) / c must
 // stay finite for any realistic table.
@@ -1537,7 +1551,9 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   const int nqb = (int)ceil_div(S, KQ::ROWS);
   const int nkb = (int)ceil_div(S, KK::ROWS);
   static_assert(KQ::ROWS == KK::ROWS && kDqNW == 4 && kDkdvNW == 4, "the pair kernel pairs equal grids");
-  if (DP <= 64 && nqb * B * H <= kPairBwdMax) {  // larger head dims: 1 workgroup of either per CU
+  const int nblk = nqb * B * H;
+  // Larger head dims: 1 workgroup of either kind per CU.
+  if (DP <= 64 && (nblk <= kPairBwdMax / 2 || (nblk <= kPairBwdMax && (2 * nblk) % (2 * kXcds) == 0))) {
     const int64_t n = (int64_t)B * H * S;
     hipLaunchKernelGGL((relpos_delta_kernel<DT>), dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st,
                        (const uint16_t*)dout, out32, delta, B, S, H, D);

@@ -186,6 +186,15 @@ def test_relpos_long_sequence(S):
     assert (dpd.sum(1).abs() <= 1e-3 * dpd.abs().sum(1) + 1e-4).all()
 
 
+@pytest.mark.parametrize("B,S,H", [(2, 1024, 16), (1, 1024, 17), (1, 640, 27), (1, 300, 16)])
+def test_relpos_backward_grid_paths(B, S, H):
+    """D = 64 backward grids around the one-launch pairing of dQ and dK/dV blocks: 256 blocks
+    of each kind (the XCD-half pairing, 32 per XCD half), 136 (17 per XCD half), 135 (an odd
+    count per XCD, so the two kernels run in separate launches) and 48 (one workgroup per CU)."""
+    log(f"relpos backward grid paths B{B} S{S} H{H} D64")
+    _check(B, S, H, 64, 0.125, ref_device="cuda")
+
+
 def test_relpos_backward_deterministic():
     log("relpos determinism B2 S512 H4 D64")
     B, S, H, D = 2, 512, 4, 64
