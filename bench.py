@@ -395,6 +395,9 @@ def bench_relpos_fwd_config4(args) -> dict:
     t = _time_steps(_rotating(lambda i: _hip.relpos_fwd(qkv_dev[i], pd, B, S, H, D, scale), nset),
                     args.steps, args.warmup, st)
     warm = _time_steps(lambda: _hip.relpos_fwd(qkv_dev[0], pd, B, S, H, D, scale), args.steps, args.warmup, st)
+    # The same forward when no backward follows (relpos_attention under no_grad): out only.
+    tn = _time_steps(_rotating(lambda i: _hip.relpos_fwd(qkv_dev[i], pd, B, S, H, D, scale, stats=False), nset),
+                     args.steps, args.warmup, st)
     fl = 4 * B * H * S * S * D
     tfl = _rate(fl, t["ms_mean"], 1e12)
     return {"workload": f"relpos attention fwd B{B} H{H} L{S} D{D} bf16 (BASELINE config 4)",
@@ -403,6 +406,9 @@ def bench_relpos_fwd_config4(args) -> dict:
             "matrix_dtype": "bf16", "rotation": f"{nset} input sets",
             "mall_warm": {"ms_per_step": round(warm["ms_mean"], 4), "TFLOP/s": round(_rate(fl, warm["ms_mean"], 1e12), 1),
                           "note": "one set, forward after forward: its 14 MB qkv stays in the caches"},
+            "no_grad": {"ms_per_step": round(tn["ms_mean"], 4), "TFLOP/s": round(_rate(fl, tn["ms_mean"], 1e12), 1),
+                        "note": "out only (no out32 or lse: nothing for a backward), what relpos_attention "
+                                "runs when no input requires grad; same rotation"},
             "roofline": _roofline(tfl, "TFLOP/s")}
 
 

@@ -143,7 +143,10 @@ int krsi_geglu_linear_fwd(const void* x, const void* w, void* out, int64_t rows,
  *      q at columns [h*D, h*D+D), k at [H*D + h*D, ...), v at [2*H*D + h*D, ...).
  * pd:  [H, 2S-1] fp32, bias[h,i,j] = pd[h, j - i + S - 1].
  * out: [B*S, H*D] of T; out32: same, fp32; lse: [B*H, S] fp32 in the log2
- *      domain (lse = log2 sum_j 2^{(q.k*scale + bias) * log2(e)}).
+ *      domain (lse = log2 sum_j 2^{(q.k*scale + bias) * log2(e)}). out32 and lse
+ *      are what the backward needs; both may be NULL (not one alone) when no
+ *      backward follows, and then only out is written (no counterpart in the
+ *      reference, whose forward always writes both).
  * Limits: D % 8 == 0 and 8 <= D <= 128, ld_qkv >= 3*H*D, rows of a multiple
  *         of 16 bytes (ld_qkv % 8 == 0 for 16-bit T, % 4 for fp32), S >= 1,
  *         and for 16-bit T S * ld_qkv * 2 < 2^31 bytes (UNSUPPORTED otherwise),

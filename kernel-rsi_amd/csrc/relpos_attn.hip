@@ -439,7 +439,8 @@ __device__ __forceinline__ void fwd_step(const uint16_t* Ks, const uint16_t* Vs,
 }
 
 // O = acc / l stored as fp32 and in the activation dtype (head-dim columns 32db + 8a + 4g
-// ..+3 of this lane's query), lse = m + log2 l.
+// ..+3 of this lane's query), lse = m + log2 l. out32 and lse_q are null together when the
+// caller wants O only (no backward to follow): then only O in the activation dtype is stored.
 template <int DT, int DP>
 __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const float* l_run,
                                           bool qvalid, int g, int64_t obase, int D,
@@ -456,14 +457,14 @@ __device__ __forceinline__ void fwd_store(const f32x16* oacc, float m_run, const
         f32x4 o;
 #pragma unroll
         for (int b4 = 0; b4 < 4; ++b4) o[b4] = oacc[db][4 * a + b4] / l;
-        *reinterpret_cast<f32x4*>(out32 + obase + d0) = o;
+        if (out32) *reinterpret_cast<f32x4*>(out32 + obase + d0) = o;
         uint2 ob;
         ob.x = Elem<DT>::pack2(o[0], o[1]);
         ob.y = Elem<DT>::pack2(o[2], o[3]);
         *reinterpret_cast<uint2*>(out + obase + d0) = ob;
       }
     }
-  if (g == 0) *lse_q = m_run + log2f(l);
+  if (g == 0 && lse_q) *lse_q = m_run + log2f(l);
 }
 
 // Staged stores. A wave's transposed accumulators (lane l32 holds row l32; register 4a + b4 of
@@ -493,7 +494,7 @@ __device__ __forceinline__ void store_rows_staged(const f32x16* acc, Op op, int 
     // Other lanes' values are read back: keep every tile write of this block before the reads
     // (the LDS executes one wave's operations in order).
     asm volatile("" ::: "memory");
-    if constexpr (W32) {
+    if (W32 && out32) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {  // fp32: 32 rows x 8 chunks of 4
         const int c = lane + 64 * k, r = c >> 3, j = c & 7;
@@ -524,7 +525,7 @@ __device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run
                                                  uint16_t* __restrict__ out, float* __restrict__ out32,
                                                  float* __restrict__ lse_q, float* wt) {
   const float l = xhalf_sum(l_run[0] + l_run[1]);
-  if ((lane >> 5) == 0 && (lane & 31) < nrows) *lse_q = m_run + log2f(l);
+  if (lse_q && (lane >> 5) == 0 && (lane & 31) < nrows) *lse_q = m_run + log2f(l);
   store_rows_staged<DT, DP, true>(oacc, [l](float x) { return x / l; }, lane, nrows, row0, HD, D, out, out32,
                                   wt);
 }
@@ -628,10 +629,10 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
     __syncthreads();  // every wave is done with the last tiles
     fwd_store_staged<DT, DP>(oacc, m_run, l_run, lane, min(32, S - (i_wg + wave * 32)),
                              (tok0 + i_wg + wave * 32) * HD + (int64_t)h * D, HD, D, out, out32,
-                             lse + (int64_t)bh * S + qi, reinterpret_cast<float*>(KVs) + wave * kWaveTile);
+                             (lse ? lse + (int64_t)bh * S + qi : nullptr), reinterpret_cast<float*>(KVs) + wave * kWaveTile);
   } else {
     fwd_store<DT, DP>(oacc, m_run, l_run, qvalid, g, (tok0 + qi) * HD + (int64_t)h * D, D, out, out32,
-                      lse + (int64_t)bh * S + qi);
+                      (lse ? lse + (int64_t)bh * S + qi : nullptr));
   }
 }
 
@@ -779,7 +780,7 @@ __global__ __launch_bounds__(512, (DP == 64 || DP <= 32 ? 4 : 2)) void relpos_fw
     asm volatile("" ::: "memory");
     fwd_store_staged<DT, DP>(oacc, m, lm, lane, min(32, S - (i_wg + gw * 32)),
                              (tok0 + i_wg + gw * 32) * HD + (int64_t)h * D, HD, D, out, out32,
-                             lse + (int64_t)bh * S + qi, reinterpret_cast<float*>(stage) + (gw * SLOTS) * 64);
+                             (lse ? lse + (int64_t)bh * S + qi : nullptr), reinterpret_cast<float*>(stage) + (gw * SLOTS) * 64);
   }
 }
 
@@ -1630,10 +1631,11 @@ int krsi_relpos_fwd(const void* qkv, int64_t ld_qkv, const float* pd, void* out,
                     int32_t dtype, void* stream) {
   using namespace krsi;
   if (dtype != kBf16 && dtype != kF16 && dtype != kF32) return KRSI_ERR_UNSUPPORTED;
-  if (!qkv || !pd || !out || !out32 || !lse) return KRSI_ERR_NULL_POINTER;
+  // out32 and lse may both be null (O only, for a forward no backward follows), not one alone.
+  if (!qkv || !pd || !out || (!out32 != !lse)) return KRSI_ERR_NULL_POINTER;
   int rc = check_attn(qkv, ld_qkv, B, S, H, D, scale, dtype == kF32 ? 4 : 2);
   if (rc != KRSI_OK) return rc;
-  if (!aligned16(out) || !aligned16(out32)) return KRSI_ERR_MISALIGNED;
+  if (!aligned16(out) || (out32 && !aligned16(out32))) return KRSI_ERR_MISALIGNED;
   hipStream_t st = as_stream(stream);
   if (dtype == kF32)
     return relpos_fwd_f32(static_cast<const float*>(qkv), ld_qkv, pd, static_cast<float*>(out), out32, lse,

@@ -282,8 +282,8 @@ __global__ __launch_bounds__(kThreadsF) void relpos_fwd_f32_kernel(
   if (qvalid) {
     const int64_t ob = ((int64_t)b * S + qi) * HD + (int64_t)h * D;
     store_dims<DB>(out + ob, oacc, 1.f / l, g, D);
-    if (out32 != out) store_dims<DB>(out32 + ob, oacc, 1.f / l, g, D);
-    if (g == 0) lse[(int64_t)bh * S + qi] = m_run + log2f(l);
+    if (out32 && out32 != out) store_dims<DB>(out32 + ob, oacc, 1.f / l, g, D);
+    if (g == 0 && lse) lse[(int64_t)bh * S + qi] = m_run + log2f(l);
   }
 }
 

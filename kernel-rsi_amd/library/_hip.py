@@ -245,13 +245,15 @@ def _check_relpos(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D
 
 
 def relpos_fwd(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: int,
-               scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """out (qkv's dtype), out32 (fp32) [B*S, H*D] and lse [B*H, S] (log2 domain)."""
+               scale: float, stats: bool = True):
+    """out (qkv's dtype), out32 (fp32) [B*S, H*D] and lse [B*H, S] (log2 domain). With
+    stats=False (a forward no backward follows) the kernels store out only: out32 and lse
+    come back as None."""
     dt = _check_relpos(qkv, pd, B, S, H, D)
     pd = pd.contiguous()
     out = torch.empty(B * S, H * D, device=qkv.device, dtype=qkv.dtype)
-    out32 = torch.empty(B * S, H * D, device=qkv.device, dtype=torch.float32)
-    lse = torch.empty(B * H, S, device=qkv.device, dtype=torch.float32)
+    out32 = torch.empty(B * S, H * D, device=qkv.device, dtype=torch.float32) if stats else None
+    lse = torch.empty(B * H, S, device=qkv.device, dtype=torch.float32) if stats else None
     _check(lib().krsi_relpos_fwd(_ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out), _ptr(out32),
                                  _ptr(lse), B, S, H, D, float(scale), dt, _stream(qkv)))
     return out, out32, lse

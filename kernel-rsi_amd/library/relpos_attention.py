@@ -11,8 +11,10 @@ relpos_attention(qkv, pd, B, S, H, D, scale) returns [B*S, H*D].
        3*H*D columns (the gradient still flows to the original tensor).
   pd   [H, 2S-1] fp32: the bias of query i and key j in head h is pd[h, j - i + S - 1]. This
        covers T5 relative positions, ALiBi and any other Toeplitz bias.
-The backward keeps the fp32 output to form delta_i = sum_d dO_id * O_id. It sums dS along its
-diagonals inside the kernels to form pd's gradient. No [B, H, S, S] tensor is ever allocated.
+The backward keeps the fp32 output to form delta_i = sum_d dO_id * O_id; a forward that no
+backward can follow (grad mode off, or neither input requiring grad) stores O alone. The
+backward sums dS along its diagonals inside the kernels to form pd's gradient. No
+[B, H, S, S] tensor is ever allocated.
 D may be any multiple of 8 up to 128 (D = 72 runs). Same public functions and arguments as the
 reference's library/relpos_attention.py:198-222; usable under torch.compile(fullgraph=True).
 """
@@ -66,6 +68,9 @@ def relpos_attention(qkv, pd, B, S, H, D, scale):
     qkv = _kernel_layout(qkv, H, D)
     if compiling():
         return _ops().relpos_fwd_op(qkv, pd, B, S, H, D, scale)[0]
+    if not (torch.is_grad_enabled() and (qkv.requires_grad or pd.requires_grad)):
+        # No backward can follow: the kernels skip the fp32 output and lse it would need.
+        return _hip.relpos_fwd(qkv, pd, B, S, H, D, scale, stats=False)[0]
     return RelPosAttention.apply(qkv, pd, B, S, H, D, scale)
 
 

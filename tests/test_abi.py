@@ -93,6 +93,10 @@ def test_validation_before_launch():
     assert lib.krsi_relpos_fwd(FAKE, 384, FAKE, FAKE + 2, FAKE, FAKE, 2, 16, 2, 64, 1e-20, 0, NULL) == E["SCALE"]
     assert fwd(S=1 << 20, ld=1024) == E["UNSUP"]  # one (batch, head) slice >= 2^31 bytes
     assert fwd(pd=NULL) == E["NULL"]
+    # out32 and lse are optional together (a forward with no backward), not one without the other.
+    assert lib.krsi_relpos_fwd_bf16(FAKE, 384, FAKE, FAKE, NULL, FAKE, 2, 16, 2, 64, 0.125, NULL) == E["NULL"]
+    assert lib.krsi_relpos_fwd_bf16(FAKE, 384, FAKE, FAKE, FAKE, NULL, 2, 16, 2, 64, 0.125, NULL) == E["NULL"]
+    assert lib.krsi_relpos_fwd_bf16(FAKE, 384, FAKE, FAKE, NULL, NULL, 2, 16, 0, 64, 0.125, NULL) == E["SHAPE"]
     assert fwd(B=40000, H=2) == E["SHAPE"]   # B*H above the grid limit
     ws = lib.krsi_relpos_bwd_workspace_bytes(args["B"], args["S"], args["H"], args["D"])
     assert lib.krsi_relpos_bwd_bf16(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 384, FAKE, FAKE, ws - 1,

@@ -186,6 +186,25 @@ def test_relpos_long_sequence(S):
     assert (dpd.sum(1).abs() <= 1e-3 * dpd.abs().sum(1) + 1e-4).all()
 
 
+@pytest.mark.parametrize("B,S,H,D,dt", [(2, 1024, 16, 72, torch.bfloat16),   # key-split forward
+                                        (4, 1024, 16, 64, torch.bfloat16),   # 4-wave forward
+                                        (2, 300, 2, 32, torch.float16),      # unstaged store (D <= 32)
+                                        (1, 200, 2, 64, torch.float32)])     # fp32 kernels
+def test_relpos_forward_without_stats(B, S, H, D, dt):
+    """The forward with out32 and lse left out (null, for a forward no backward follows) stores
+    bitwise the same output, writes nothing else, and is what relpos_attention runs when no
+    input requires grad or grad mode is off."""
+    log(f"relpos forward without stats B{B} S{S} H{H} D{D} {dt}")
+    qkv = seeded((B * S, 3 * H * D), 3, dtype=dt)
+    pd = seeded((H, 2 * S - 1), 4, std=0.02, dtype=torch.float32)
+    want, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, 0.125)
+    got, o32, l2 = _hip.relpos_fwd(qkv, pd, B, S, H, D, 0.125, stats=False)
+    assert o32 is None and l2 is None and torch.equal(got, want)
+    assert torch.equal(A.relpos_attention(qkv, pd, B, S, H, D, 0.125), want)
+    with torch.no_grad():
+        assert torch.equal(A.relpos_attention(qkv.requires_grad_(True), pd, B, S, H, D, 0.125), want)
+
+
 @pytest.mark.parametrize("B,S,H", [(2, 1024, 16), (1, 1024, 17), (1, 640, 27), (1, 300, 16)])
 def test_relpos_backward_grid_paths(B, S, H):
     """D = 64 backward grids around the one-launch pairing of dQ and dK/dV blocks: 256 blocks
