@@ -23,7 +23,7 @@ INCLUDE = ROOT / "include"
 OBJDIR = HERE / "_build"
 LIB = HERE / "libkrsi_hip.so"
 # The streaming-bandwidth probe of hw.py: its own library, not part of the kernel library.
-PROBE_SRC = HERE / "probe" / "stream_probe.hip"
+PROBE_SRCS = [HERE / "probe" / "stream_probe.hip", HERE / "probe" / "lds_probe.hip"]
 PROBE_LIB = HERE / "libkrsi_probe.so"
 ARCH = "gfx950"
 
@@ -84,7 +84,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
     tmp = PROBE_LIB.with_suffix(".so.tmp")
-    _run([hipcc, *HIP_FLAGS, "-shared", "-o", str(tmp), str(PROBE_SRC)], verbose)
+    _run([hipcc, *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, PROBE_SRCS)], verbose)
     os.replace(tmp, PROBE_LIB)
     return LIB
 

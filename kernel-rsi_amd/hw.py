@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Measured ceilings of this GPU, written to hardware/<gpu>.json.
 
-  python kernel-rsi_amd/hw.py [--quick] [--stream-only]
+  python kernel-rsi_amd/hw.py [--quick] [--stream-only] [--lds-only] [--lds-banks]
 
 The reference's tools read two things from such a record: `tflops[dtype]` and
 `bw_copy_gbs` / `bw_read_gbs` (tools/common.py:56-64; its own probe is tools/hw.py). They use
@@ -12,6 +12,9 @@ package's roofline discussion uses:
     practical HBM ceiling for bandwidth-bound kernels, which torch's copy does not reach;
   * the rate of each bandwidth-bound kernel's own access pattern with trivial arithmetic
     (the row-pattern probes of libkrsi_probe.so), the ceiling that kernel is measured against;
+  * LDS bytes per clock per CU of each access form the attention kernels use (the LDS probes
+    of libkrsi_probe.so; `--lds-banks` runs the bank-pattern probe that
+    probe/lds_banks.py fits under a counter run);
   * launch costs;
   * the ridge points.
 The probes are a table of small functions. Each runs under `Clock`, which reports the median
@@ -234,6 +237,70 @@ def probe_patterns(clock: Clock, quick: bool = False) -> dict:
     return res
 
 
+LDS_FORMS = ("ds_read_b128", "ds_read_b64", "ds_read_b64_tr_b16", "ds_read_b32", "ds_write_b32",
+             "ds_write_b64", "ds_write_b128", "ds_add_f32", "ds_read_b128 half-wave broadcast")
+
+
+def _probe_lib():
+    import ctypes  # noqa: PLC0415
+
+    path = HERE / "libkrsi_probe.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: run kernel-rsi_amd/build.py first")
+    lib = ctypes.CDLL(str(path))
+    lib.krsi_probe_lds_rate.restype = ctypes.c_int
+    lib.krsi_probe_lds_rate.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 3
+    lib.krsi_probe_lds_form_bytes.restype = ctypes.c_int
+    lib.krsi_probe_lds_form_bytes.argtypes = [ctypes.c_int]
+    lib.krsi_probe_lds_banks.restype = ctypes.c_int
+    lib.krsi_probe_lds_banks.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_void_p]
+    return lib
+
+
+def probe_lds(quick: bool = False) -> dict:
+    """LDS bytes per clock per CU of each access form (libkrsi_probe.so krsi_probe_lds_rate): one
+    workgroup per CU, 8 and 16 waves, each wave 8 independent accesses per wait; clocks are each
+    workgroup's s_memtime cycles over its loop, averaged over the CUs."""
+    lib = _probe_lib()
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream().cuda_stream
+    cycles = torch.zeros(ncu, dtype=torch.int64, device="cuda")
+    out = {}
+    for threads in (512, 1024):
+        sink = torch.empty(ncu * threads, dtype=torch.int32, device="cuda")
+        for form, name in enumerate(LDS_FORMS):
+            iters = 128 if form == 7 else (1024 if quick else 4096)
+            for it in (8, iters):  # a short warm-up launch, then the timed one
+                if lib.krsi_probe_lds_rate(form, ncu, threads, it, sink.data_ptr(), cycles.data_ptr(), stream) != 0:
+                    raise RuntimeError(f"krsi_probe_lds_rate({form}, {ncu}, {threads}, {it}) failed")
+            torch.cuda.synchronize()
+            mean_cyc = cycles.double().mean().item()
+            nbytes = iters * 8 * lib.krsi_probe_lds_form_bytes(form) * (threads // 64)
+            out.setdefault(name, {})[f"{threads // 64} waves/CU"] = round(nbytes / mean_cyc, 1)
+    return out
+
+
+def lds_bank_patterns_run(iters: int = 100) -> int:
+    """Launch the bank-pattern probe once per pattern of probe/lds_banks.py (one wave each), for a
+    counter run: rocprofv3 --kernel-trace --pmc SQ_LDS_BANK_CONFLICT SQ_INSTS_LDS -- python3
+    kernel-rsi_amd/hw.py --lds-banks. Returns the number of patterns."""
+    sys.path.insert(0, str(HERE / "probe"))
+    import lds_banks  # noqa: PLC0415
+
+    pats = lds_banks.patterns()
+    for p in pats:
+        assert len(p) == 64 and all(a % 16 == 0 and 0 <= a < 32768 - 16 for a in p), "pattern out of range"
+    lib = _probe_lib()
+    addr = torch.tensor([a for p in pats for a in p], dtype=torch.int32, device="cuda")
+    sink = torch.empty(64, dtype=torch.int32, device="cuda")
+    if lib.krsi_probe_lds_banks(addr.data_ptr(), len(pats), iters, sink.data_ptr(),
+                                torch.cuda.current_stream().cuda_stream) != 0:
+        raise RuntimeError("krsi_probe_lds_banks failed")
+    torch.cuda.synchronize()
+    return len(pats)
+
+
 def probe_launch(clock: Clock) -> dict:
     """Microseconds per tiny kernel: one stream launch of a torch op, one graph replay."""
     x = torch.zeros(1, device="cuda")
@@ -263,6 +330,7 @@ def collect(quick: bool = False) -> dict:
     rec.update(probe_bandwidth(clock))
     rec["stream_kernel_gbs"] = probe_stream(clock, quick)
     rec["pattern_probe_gbs"] = probe_patterns(clock, quick)
+    rec["lds_bytes_per_clk_per_cu"] = probe_lds(quick)
     stream_bw = max(rec["bw_copy_gbs"], rec["bw_read_gbs"])
     rec["ridge_flop_per_byte"] = {k: round(v * 1e3 / stream_bw, 1) for k, v in tflops.items()
                                   if isinstance(v, (int, float))}
@@ -293,9 +361,19 @@ def main(argv=None) -> int:
     ap.add_argument("--out-dir", type=Path, default=HERE / "hardware", help="where the record goes")
     ap.add_argument("--stream-only", action="store_true",
                     help="only the streaming-kernel ceilings, printed, no record written")
+    ap.add_argument("--lds-only", action="store_true", help="only the LDS rates, printed, no record written")
+    ap.add_argument("--lds-banks", action="store_true",
+                    help="only the bank-pattern probe's launches (for a counter run), no record written")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("hw.py measures a GPU; none is visible")
+    if args.lds_banks:
+        print(f"launched {lds_bank_patterns_run()} bank patterns", flush=True)
+        return 0
+    if args.lds_only:
+        for name, v in probe_lds(args.quick).items():
+            print(f"{name}: {v}", flush=True)
+        return 0
     if args.stream_only:
         for mix, v in probe_stream(Clock(samples=5), args.quick).items():
             print(f"{mix}: {v}", flush=True)
