@@ -100,16 +100,37 @@ def _queue_head_start() -> None:
         _PAD[0].fill_(0.0)
 
 
+SETTLE_MS = 30.0  # untimed GPU work queued right before each timed region
+SETTLE_MAX_STEPS = 400
+
+
 def _time_steps(step, steps: int, warmup: int, stream: torch.cuda.Stream) -> dict:
     """Warm up, then time exactly `steps` back-to-back calls of step(), bracketed by synchronize.
     One pair of HIP events on the kernels' stream goes around all of them. Returns the mean GPU
     ms per step (from the events) and the host's ms per step to enqueue them.
 
     One pair, not one per step: event records between steps leave the GPU idle for ~10 us each
-    (kernel trace: 10-11 us gaps before every step's first kernel)."""
+    (kernel trace: 10-11 us gaps before every step's first kernel).
+
+    Settle run: the synchronize between warm-up and timing leaves the GPU idle while the host
+    sets up, and its clocks then take ~20-30 ms of sustained load to come back. Measured on
+    config 5's step after a 30 ms idle gap: the first 20 steps average 1.533 ms, steps 40-60
+    1.421 ms, so timing from an idle start reported 1.51-1.52 ms per step where a continuous
+    training loop runs at 1.42. So after the synchronize the GPU first gets untimed settle
+    steps totalling about SETTLE_MS of its time (sized from the warm-up, at most
+    SETTLE_MAX_STEPS), then the head-start fills, then the timed steps."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
+    step()
+    w1.record(stream)
+    torch.cuda.synchronize()
+    one = max(w0.elapsed_time(w1), 1e-3)
+    settle = min(SETTLE_MAX_STEPS, math.ceil(SETTLE_MS / one))
+    for _ in range(settle):
+        step()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     _queue_head_start()
     a.record(stream)
@@ -119,7 +140,7 @@ def _time_steps(step, steps: int, warmup: int, stream: torch.cuda.Stream) -> dic
     host = (time.perf_counter() - t0) * 1e3 / steps
     b.record(stream)
     torch.cuda.synchronize()
-    return {"ms_mean": a.elapsed_time(b) / steps, "host_ms": host}
+    return {"ms_mean": a.elapsed_time(b) / steps, "host_ms": host, "settle_steps": settle}
 
 
 def _rotating(fn, nset: int):
@@ -693,6 +714,9 @@ def main() -> None:
     line = {
         "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
+        "timing": (f"per leg: {args.warmup} warm-up steps, synchronize, untimed settle steps worth ~{SETTLE_MS:g} ms "
+                   f"of GPU time (clocks back at steady state), head-start fills, then {args.steps} timed steps "
+                   "between one pair of HIP events"),
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded CPU randn, BASELINE shapes)",
         "config": {"workload": head["workload"], "device": torch.cuda.get_device_name(0)},
         "roofline": head["roofline"],
