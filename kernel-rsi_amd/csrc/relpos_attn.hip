@@ -647,8 +647,10 @@ __global__ __launch_bounds__(64 * NW, (DP == 64 ? 4 : 2)) void relpos_fwd_kernel
 // which merges them: m = max(m0, m1), x = x0 2^(m0 - m) + x1 2^(m1 - m) for l and O. Each
 // half keeps its own running reference point, so p of the second half is rounded relative to
 // that half's reference point rather than to one carried over all earlier keys.
-template <int DT, int DP>
-__global__ __launch_bounds__(512, (DP == 64 || DP <= 32 ? 4 : 2)) void relpos_fwd_ks_kernel(
+// WIDE: the grid has at most one workgroup per CU, so nothing is gained by leaving registers for
+// a second one (at D 49-64: 172 VGPRs and no spills, against 128 and 72 bytes spilled).
+template <int DT, int DP, bool WIDE>
+__global__ __launch_bounds__(512, (!WIDE && (DP == 64 || DP <= 32) ? 4 : 2)) void relpos_fwd_ks_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     uint16_t* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse, int S, int H,
     int D, Fold f) {
@@ -1474,6 +1476,11 @@ constexpr int kFwdNW = 4;
 // Forward grids of fewer workgroups than this (two per CU of the MI355X's 256) split each
 // workgroup's keys over two wave groups (relpos_fwd_ks_kernel).
 constexpr unsigned kFwdSplitBelow = 512;
+// Split-key grids of at most this many workgroups (one per CU) take the kernel's register
+// budget for 2 waves per SIMD at D 49-64 instead of 4. Interleaved A/B of the forward: B4 S512
+// H16 D64 14.80 -> 14.42 us, B2 S1024 H16 21.0 -> 20.0 us, B1 S2048 H16 34.6 -> 32.2 us, B1 S300
+// H16 10.2 -> 9.45 us; at 384 workgroups it holds one per CU and lost (29.3 -> 35.6 us).
+constexpr unsigned kFwdWideMax = 256;
 constexpr int kDqNW = 4;
 constexpr int kDkdvNW = 4;
 // Backward grids of at most this many workgroups per kernel (the MI355X's 256 CUs) run the dQ
@@ -1533,8 +1540,15 @@ void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* 
   using K = Blk<kFwdNW>;
   const dim3 grid((unsigned)(ceil_div(S, K::ROWS) * B * H));
   if (grid.x < kFwdSplitBelow && S > kStep) {
-    hipLaunchKernelGGL((relpos_fwd_ks_kernel<DT, DP>), grid, dim3(2 * K::NT), 0, st, (const uint16_t*)qkv,
-                       ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
+    if constexpr (DP == 64) {
+      if (grid.x <= kFwdWideMax) {
+        hipLaunchKernelGGL((relpos_fwd_ks_kernel<DT, DP, true>), grid, dim3(2 * K::NT), 0, st,
+                           (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
+        return;
+      }
+    }
+    hipLaunchKernelGGL((relpos_fwd_ks_kernel<DT, DP, false>), grid, dim3(2 * K::NT), 0, st,
+                       (const uint16_t*)qkv, ld, pd, (uint16_t*)out, out32, lse, S, H, D, f);
     return;
   }
   hipLaunchKernelGGL((relpos_fwd_kernel<DT, DP, kFwdNW>), grid, dim3(K::NT), 0, st,

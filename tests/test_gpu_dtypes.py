@@ -165,6 +165,9 @@ def test_relpos_fp16_strided_and_large():
     _relpos_fp16(2, 96, 2, 64, 0.125, ld_extra=40)
     log("relpos fp16 B2 S1024 H16 D72")
     _relpos_fp16(2, 1024, 16, 72, 1 / math.sqrt(72), ref_device="cuda")
+    # D 64 with 256 blocks of each backward kind: the one-launch dQ + dK/dV pairing.
+    log("relpos fp16 B2 S1024 H16 D64")
+    _relpos_fp16(2, 1024, 16, 64, 0.125, ref_device="cuda")
 
 
 def _relpos_fp32(B, S, H, D, scale, std=1.0, pd_std=0.02, ref_device="cpu", ld_extra=0, seed=70,
