@@ -1326,34 +1326,41 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
 }
 
 // --------------------------------------------- backward on small grids: one launch for both
-// delta[bh, i] = sum_d dO[i, d] O32[i, d] for one (query, head) per thread, summed exactly as the
-// dQ kernel's prologue sums it (the lower half-wave's 8-element chunks 16s..16s+7, the upper
-// half's 16s+8..16s+15, each in order, then lower + upper), so delta is bitwise the same.
+// delta[bh, i] = sum_d dO[i, d] O32[i, d], summed exactly as the dQ kernel's prologue sums it
+// (the lower half-wave's 8-element chunks 16s..16s+7, the upper half's 16s+8..16s+15, each in
+// order, then lower + upper), so delta is bitwise the same. Two threads per (query, head), one
+// per half; the even one adds the odd one's sum to its own. D <= 64 (the paired backward's).
 template <int DT>
 __global__ __launch_bounds__(256) void relpos_delta_kernel(const uint16_t* __restrict__ dout,
                                                            const float* __restrict__ out32,
                                                            float* __restrict__ delta_ws, int B, int S, int H,
                                                            int D) {
   const int64_t n = (int64_t)B * H * S;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  const int64_t bh = e / S, i = e - bh * S;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int g = (int)(t & 1);
+  const int64_t e = t >> 1;
+  const bool live = e < n;
+  const int64_t ec = live ? e : 0;
+  const int64_t bh = ec / S, i = ec - bh * S;
   const int64_t b = bh / H, h = bh - b * H;
   const int64_t base = (b * S + i) * H * D + h * D;
-  float half[2] = {0.f, 0.f};
+  float half = 0.f;
 #pragma unroll
-  for (int g = 0; g < 2; ++g)
-    for (int d0 = 8 * g; d0 < D; d0 += 16) {
+  for (int s = 0; s < 4; ++s) {
+    const int d0 = 16 * s + 8 * g;
+    if (live && d0 < D) {
       float df[8];
       Elem<DT>::unpack(ld16(dout + base + d0), df);
       const f32x4 o0 = *reinterpret_cast<const f32x4*>(out32 + base + d0);
       const f32x4 o1 = *reinterpret_cast<const f32x4*>(out32 + base + d0 + 4);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) half[g] += df[q] * o0[q];
+      for (int q = 0; q < 4; ++q) half += df[q] * o0[q];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) half[g] += df[4 + q] * o1[q];
+      for (int q = 0; q < 4; ++q) half += df[4 + q] * o1[q];
     }
-  delta_ws[e] = half[0] + half[1];
+  }
+  const float upper = __shfl_xor(half, 1);
+  if (live && g == 0) delta_ws[e] = half + upper;
 }
 
 // The dQ and dK/dV kernels in one grid, for grids too small to give every CU two workgroups
@@ -1570,7 +1577,7 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   // Larger head dims: 1 workgroup of either kind per CU.
   if (DP <= 64 && (nblk <= kPairBwdMax / 2 || (nblk <= kPairBwdMax && (2 * nblk) % (2 * kXcds) == 0))) {
     const int64_t n = (int64_t)B * H * S;
-    hipLaunchKernelGGL((relpos_delta_kernel<DT>), dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st,
+    hipLaunchKernelGGL((relpos_delta_kernel<DT>), dim3((unsigned)ceil_div(2 * n, 256)), dim3(256), 0, st,
                        (const uint16_t*)dout, out32, delta, B, S, H, D);
     hipLaunchKernelGGL((relpos_bwd_pair_kernel<DT, DP>), dim3((unsigned)(2 * nqb * B * H)), dim3(256), 0, st,
                        (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32, lse, delta, (uint16_t*)dqkv,
