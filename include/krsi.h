@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define KRSI_ABI_VERSION 2
+#define KRSI_ABI_VERSION 3
 
 /* Activation dtypes. The reference's Triton kernels are dtype-generic, and so is
  * every entry point here. */
@@ -169,8 +169,18 @@ int krsi_relpos_fwd_bf16(const void* qkv, int64_t ld_qkv, const float* pd, void*
  * layout as qkv, every q/k/v column written); dpd: [H, 2S-1] fp32 (overwritten).
  * P and dS are rounded to T before their products (:88-92, :125); for fp32
  * that is no rounding. ld_dqkv rows are a multiple of 16 bytes too.
- * workspace: at least krsi_relpos_bwd_workspace_bytes(B,S,H,D) bytes.        */
+ * workspace: krsi_relpos_bwd_workspace_bytes(B,S,H,D) bytes (grows as B H S^2
+ * / 32: the dpd partial rows of every 128-key block) for the fastest path, or
+ * anything down to krsi_relpos_bwd_workspace_min_bytes(B,S,H,D) (grows as
+ * B H S: one block's rows). A smaller workspace runs the dK/dV kernel over as
+ * many key blocks per launch as it holds, each launch's rows summed into dpd
+ * before the next; dqkv is bitwise the same, dpd is the same sum in another
+ * order (differences at fp32 rounding). Smaller than the minimum:
+ * KRSI_ERR_WORKSPACE. The minimum has no counterpart in the reference (whose
+ * backward materialises dbias [B,H,S,S]); it is for long-context callers that
+ * must bound the backward's memory.                                          */
 size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t D);
+size_t krsi_relpos_bwd_workspace_min_bytes(int32_t B, int32_t S, int32_t H, int32_t D);
 int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
                     const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv, float* dpd,
                     void* workspace, size_t workspace_bytes, int32_t B, int32_t S, int32_t H,

@@ -1095,7 +1095,7 @@ __device__ __forceinline__ void bwd_dkdv_body(
     int tile, unsigned char* lds, const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd,
-    float* __restrict__ part, int S, int H, int D, Fold f, float scale) {
+    float* __restrict__ part, int S, int H, int D, Fold f, float scale, int kb0, int nkc) {
   using G = Geo<DP>;
   using K = Blk<NW>;
   using LY = DkdvLds<DP, NW>;
@@ -1115,9 +1115,10 @@ __device__ __forceinline__ void bwd_dkdv_body(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   TileLane<DP> L;
   L.init(lane);
-  const int nkb = (S + K::ROWS - 1) / K::ROWS;
-  const int bh = tile / nkb, b = bh / H, h = bh - b * H;
-  const int kblk = tile - bh * nkb;
+  // Key blocks [kb0, kb0 + nkc) of every (batch, head), nkc per (batch, head) in the grid.
+  const int bh = tile / nkc, b = bh / H, h = bh - b * H;
+  const int kbl = tile - bh * nkc;
+  const int kblk = kb0 + kbl;
   const int j_wg = kblk * K::ROWS;
   const int kk = wave * 32 + kperm(l32);  // this lane's key (score tile column l32)
   const int kj = j_wg + kk;
@@ -1154,7 +1155,7 @@ __device__ __forceinline__ void bwd_dkdv_body(
   const int rcopy = (kk + S) & 1;
   // Keys past S have p != 0 (their bias is real) but no dpd term: their ds go to a sink.
   float* myring = kvalid ? ring + ring_base(2 * wave + g, rcopy, off1) : sink;
-  float* prow = part + ((int64_t)bh * nkb + kblk) * (S + K::ROWS);
+  float* prow = part + ((int64_t)bh * nkc + kbl) * (S + K::ROWS);
 
   uint32_t qoff[Dma<DP, K::NT>::GPT], ooff[Dma<DP, K::NT>::GPT];
   dma_offsets<DP, K::NT>(qoff, ld, D);
@@ -1319,10 +1320,10 @@ __global__ __launch_bounds__(64 * NW, (DP <= 64 ? 2 : 1)) void relpos_bwd_dkdv_k
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ delta_ws, uint16_t* __restrict__ dqkv, int64_t ldd,
-    float* __restrict__ part, int S, int H, int D, Fold f, float scale) {
+    float* __restrict__ part, int S, int H, int D, Fold f, float scale, int kb0, int nkc) {
   __shared__ __attribute__((aligned(256))) unsigned char lds[DkdvLds<DP, NW>::BYTES];
   bwd_dkdv_body<DT, DP, NW>(xcd_tile(blockIdx.x, gridDim.x), lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd,
-                            part, S, H, D, f, scale);
+                            part, S, H, D, f, scale, kb0, nkc);
 }
 
 // --------------------------------------------- backward on small grids: one launch for both
@@ -1388,18 +1389,20 @@ __global__ __launch_bounds__(256, (DP <= 64 ? 2 : 1)) void relpos_bwd_pair_kerne
     idx = x * half + k - kind * half;
   }
   if (kind)
-    bwd_dkdv_body<DT, DP, 4>(idx, lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd, part, S, H, D, f, scale);
+    bwd_dkdv_body<DT, DP, 4>(idx, lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd, part, S, H, D, f, scale, 0,
+                             (S + 127) / 128);
   else
     bwd_dq_body<DT, DP, 4, true>(idx, lds, qkv, ld, pd, dout, out32, lse, delta_ws, dqkv, ldd, S, H, D, f,
                                  scale);
 }
 
-// dpd[h, k] = sum over b and key blocks of the partial rows (row of key block kb holds
-// k - rows kb), fixed order. Block: 64 diagonals (lane) of head h; the 4 waves take every
-// 4th (b, key block) term, then the 4 wave sums are added in wave order.
+// dpd[h, k] (+)= sum over b and key blocks kb0 .. kb0 + nqb - 1 of the partial rows (row of
+// key block kb holds k - rows kb; part holds the rows of those nqb blocks only), fixed order.
+// Block: 64 diagonals (lane) of head h; the 4 waves take every 4th (b, key block) term, then
+// the 4 wave sums are added in wave order; acc_in adds the total to dpd's value.
 __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict__ part,
                                                          float* __restrict__ dpd, int B, int S,
-                                                         int H, int nqb, int rows) {
+                                                         int H, int kb0, int nqb, int rows, int acc_in) {
   __shared__ float s[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + lane;
@@ -1418,9 +1421,9 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int e = e0 + 4 * i;
-        const int b = e / nqb, kb = e - b * nqb;
-        const int r = k - rows * kb;
-        v[i] = (e < terms && r >= 0 && r < rlen) ? part[((int64_t)(b * H + h) * nqb + kb) * RS + r] : 0.f;
+        const int b = e / nqb, kbl = e - b * nqb;
+        const int r = k - rows * (kb0 + kbl);
+        v[i] = (e < terms && r >= 0 && r < rlen) ? part[((int64_t)(b * H + h) * nqb + kbl) * RS + r] : 0.f;
       }
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) acc += v[i];
@@ -1428,8 +1431,11 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
   }
   s[wave][lane] = acc;
   __syncthreads();
-  if (wave == 0 && k < npd)
-    dpd[(int64_t)h * npd + k] = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
+  if (wave == 0 && k < npd) {
+    const float t = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
+    float* o = dpd + (int64_t)h * npd + k;
+    *o = acc_in ? *o + t : t;
+  }
 }
 
 // The same sum, 4 consecutive diagonals per lane with 128-bit loads, for S % 4 == 0 (then
@@ -1438,7 +1444,7 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce(const float* __restrict
 // bitwise the same; entries at or past the row's end (index rlen) are masked to 0.
 __global__ __launch_bounds__(256) void relpos_dpd_reduce4(const float* __restrict__ part,
                                                           float* __restrict__ dpd, int B, int S,
-                                                          int H, int nqb, int rows) {
+                                                          int H, int kb0, int nqb, int rows, int acc_in) {
   __shared__ f32x4 s[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int k0 = 4 * (blockIdx.x * 64 + lane);
@@ -1455,10 +1461,10 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce4(const float* __restric
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int e = e0 + 4 * i;
-        const int b = e / nqb, kb = e - b * nqb;
-        const int r = k0 - rows * kb;
+        const int b = e / nqb, kbl = e - b * nqb;
+        const int r = k0 - rows * (kb0 + kbl);
         v[i] = (e < terms && r >= 0 && r < rlen)
-                   ? *reinterpret_cast<const f32x4*>(part + ((int64_t)(b * H + h) * nqb + kb) * RS + r)
+                   ? *reinterpret_cast<const f32x4*>(part + ((int64_t)(b * H + h) * nqb + kbl) * RS + r)
                    : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1474,7 +1480,10 @@ __global__ __launch_bounds__(256) void relpos_dpd_reduce4(const float* __restric
     const f32x4 t = ((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (k0 + j < npd) dpd[(int64_t)h * npd + k0 + j] = t[j];
+      if (k0 + j < npd) {
+        float* o = dpd + (int64_t)h * npd + k0 + j;
+        *o = acc_in ? *o + t[j] : t[j];
+      }
   }
 }
 
@@ -1564,8 +1573,8 @@ void launch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float* 
 
 template <int DT, int DP>
 void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
-                const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S, int H,
-                int D, Fold f, float scale, hipStream_t st) {
+                const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int nkc, int B, int S,
+                int H, int D, Fold f, float scale, hipStream_t st) {
   using KQ = Blk<kDqNW>;
   using KK = Blk<kDkdvNW>;
   float* delta = static_cast<float*>(ws);
@@ -1575,23 +1584,29 @@ void launch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, 
   static_assert(KQ::ROWS == KK::ROWS && kDqNW == 4 && kDkdvNW == 4, "the pair kernel pairs equal grids");
   const int nblk = nqb * B * H;
   // Larger head dims: 1 workgroup of either kind per CU.
-  if (DP <= 64 && (nblk <= kPairBwdMax / 2 || (nblk <= kPairBwdMax && (2 * nblk) % (2 * kXcds) == 0))) {
+  if (DP <= 64 && nkc == nkb &&
+      (nblk <= kPairBwdMax / 2 || (nblk <= kPairBwdMax && (2 * nblk) % (2 * kXcds) == 0))) {
     const int64_t n = (int64_t)B * H * S;
     hipLaunchKernelGGL((relpos_delta_kernel<DT>), dim3((unsigned)ceil_div(2 * n, 256)), dim3(256), 0, st,
                        (const uint16_t*)dout, out32, delta, B, S, H, D);
     hipLaunchKernelGGL((relpos_bwd_pair_kernel<DT, DP>), dim3((unsigned)(2 * nqb * B * H)), dim3(256), 0, st,
                        (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32, lse, delta, (uint16_t*)dqkv,
                        ldd, part, S, H, D, f, scale);
-    launch_dpd_reduce(part, dpd, B, S, H, st);
+    launch_dpd_reduce(part, dpd, B, S, H, 0, nkb, false, st);
     return;
   }
   hipLaunchKernelGGL((relpos_bwd_dq_kernel<DT, DP, kDqNW>), dim3((unsigned)(nqb * B * H)),
                      dim3(KQ::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, out32,
                      lse, delta, (uint16_t*)dqkv, ldd, S, H, D, f, scale);
-  hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DT, DP, kDkdvNW>), dim3((unsigned)(nkb * B * H)),
-                     dim3(KK::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
-                     (const float*)delta, (uint16_t*)dqkv, ldd, part, S, H, D, f, scale);
-  launch_dpd_reduce(part, dpd, B, S, H, st);
+  // A workspace that holds the partial rows of nkc < nkb key blocks: the key blocks go in
+  // chunks of nkc, each one's rows summed into dpd before the next chunk overwrites them.
+  for (int kb0 = 0; kb0 < nkb; kb0 += nkc) {
+    const int n = min(nkc, nkb - kb0);
+    hipLaunchKernelGGL((relpos_bwd_dkdv_kernel<DT, DP, kDkdvNW>), dim3((unsigned)(n * B * H)),
+                       dim3(KK::NT), 0, st, (const uint16_t*)qkv, ld, pd, (const uint16_t*)dout, lse,
+                       (const float*)delta, (uint16_t*)dqkv, ldd, part, S, H, D, f, scale, kb0, n);
+    launch_dpd_reduce(part, dpd, B, S, H, kb0, n, kb0 > 0, st);
+  }
 }
 
 template <int DT>
@@ -1613,13 +1628,13 @@ int dispatch_fwd(const void* qkv, int64_t ld, const float* pd, void* out, float*
 
 template <int DT>
 int dispatch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd, const float* out32,
-                 const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int B, int S,
+                 const float* lse, void* dqkv, int64_t ldd, float* dpd, void* ws, int nkc, int B, int S,
                  int H, int D, Fold f, float scale, hipStream_t st) {
   switch (padded_dim(D)) {
 #define KRSI_CASE(DPV_)                                                                          \
   case DPV_:                                                                                     \
-    launch_bwd<DT, DPV_>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, dpd, ws, B, S, H, D, f, scale, \
-                         st);                                                                    \
+    launch_bwd<DT, DPV_>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, dpd, ws, nkc, B, S, H, D, f,  \
+                         scale, st);                                                             \
     break;
     KRSI_CASE(16) KRSI_CASE(32) KRSI_CASE(48) KRSI_CASE(64) KRSI_CASE(80) KRSI_CASE(96)
     KRSI_CASE(112) KRSI_CASE(128)
@@ -1632,15 +1647,26 @@ int dispatch_bwd(const void* dout, const void* qkv, int64_t ld, const float* pd,
 
 }  // namespace
 
-void launch_dpd_reduce(const float* part, float* dpd, int B, int S, int H, hipStream_t st) {
-  const int nkb = (int)ceil_div(S, kKvRows);
+void launch_dpd_reduce(const float* part, float* dpd, int B, int S, int H, int kb0, int nkc,
+                       bool acc_in, hipStream_t st) {
   if (S % 4 == 0) {
     const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 256), (unsigned)H);
-    hipLaunchKernelGGL(relpos_dpd_reduce4, rgrid, dim3(256), 0, st, part, dpd, B, S, H, nkb, kKvRows);
+    hipLaunchKernelGGL(relpos_dpd_reduce4, rgrid, dim3(256), 0, st, part, dpd, B, S, H, kb0, nkc, kKvRows,
+                       (int)acc_in);
   } else {
     const dim3 rgrid((unsigned)ceil_div(2 * S - 1, 64), (unsigned)H);
-    hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, part, dpd, B, S, H, nkb, kKvRows);
+    hipLaunchKernelGGL(relpos_dpd_reduce, rgrid, dim3(256), 0, st, part, dpd, B, S, H, kb0, nkc, kKvRows,
+                       (int)acc_in);
   }
+}
+
+int relpos_bwd_chunk_blocks(size_t ws_bytes, int B, int S, int H) {
+  const size_t delta = ws_delta_bytes(B, S, H);
+  if (ws_bytes < delta) return 0;
+  const size_t row_set = (size_t)B * H * (size_t)(S + kKvRows) * sizeof(float);
+  const size_t fit = (ws_bytes - delta) / row_set;
+  const int nkb = (int)ceil_div(S, kKvRows);
+  return fit >= (size_t)nkb ? nkb : (int)fit;
 }
 
 }  // namespace krsi
@@ -1680,6 +1706,13 @@ size_t krsi_relpos_bwd_workspace_bytes(int32_t B, int32_t S, int32_t H, int32_t 
   return ws_delta_bytes(B, S, H) + ws_part_bytes(B, S, H);
 }
 
+size_t krsi_relpos_bwd_workspace_min_bytes(int32_t B, int32_t S, int32_t H, int32_t D) {
+  using namespace krsi;
+  (void)D;
+  if (B <= 0 || S <= 0 || H <= 0) return 0;
+  return ws_delta_bytes(B, S, H) + (size_t)B * H * (size_t)(S + kKvRows) * sizeof(float);
+}
+
 int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,
                     const float* out32, const float* lse, void* dqkv, int64_t ld_dqkv, float* dpd,
                     void* workspace, size_t workspace_bytes, int32_t B, int32_t S, int32_t H,
@@ -1693,22 +1726,26 @@ int krsi_relpos_bwd(const void* dout, const void* qkv, int64_t ld_qkv, const flo
   if (ld_dqkv < 3 * (int64_t)H * D) return KRSI_ERR_BAD_SHAPE;
   if ((ld_dqkv * esize) % 16 != 0 || !aligned16(dqkv) || !aligned16(dout) || !aligned16(out32))
     return KRSI_ERR_MISALIGNED;
-  if (!workspace || workspace_bytes < krsi_relpos_bwd_workspace_bytes(B, S, H, D))
+  if (!workspace || workspace_bytes < krsi_relpos_bwd_workspace_min_bytes(B, S, H, D))
     return KRSI_ERR_WORKSPACE;
   if (!aligned16(workspace)) return KRSI_ERR_MISALIGNED;
+  // Key blocks per dK/dV launch: all of them with the full workspace, fewer (then several
+  // launches, each followed by its dpd sum) with a smaller one.
+  const int nkc = relpos_bwd_chunk_blocks(workspace_bytes, B, S, H);
   hipStream_t st = as_stream(stream);
   if (dtype == kF32) {
     float* delta = static_cast<float*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws_delta_bytes(B, S, H));
     return relpos_bwd_f32(static_cast<const float*>(dout), static_cast<const float*>(qkv), ld_qkv, pd, out32,
-                          lse, static_cast<float*>(dqkv), ld_dqkv, dpd, delta, part, B, S, H, D, scale, st);
+                          lse, static_cast<float*>(dqkv), ld_dqkv, dpd, delta, part, nkc, B, S, H, D, scale,
+                          st);
   }
   const Fold f = fold_scale(scale);
   return dtype == kF16
              ? dispatch_bwd<kF16>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace,
-                                  B, S, H, D, f, scale, st)
+                                  nkc, B, S, H, D, f, scale, st)
              : dispatch_bwd<kBf16>(dout, qkv, ld_qkv, pd, out32, lse, dqkv, ld_dqkv, dpd, workspace,
-                                   B, S, H, D, f, scale, st);
+                                   nkc, B, S, H, D, f, scale, st);
 }
 
 int krsi_relpos_bwd_bf16(const void* dout, const void* qkv, int64_t ld_qkv, const float* pd,

@@ -380,7 +380,8 @@ template <int DB>
 __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ pd,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta_ws,
-    float* __restrict__ dqkv, int64_t ldd, float* __restrict__ part, int S, int H, int D, float scale) {
+    float* __restrict__ dqkv, int64_t ldd, float* __restrict__ part, int S, int H, int D, float scale,
+    int kb0, int nkc) {
   using G = GeoF<DB>;
   // The dS block [query][key] sits at columns kStepF .. kStepF + kRowsF - 1 of rows of DSL
   // floats whose other columns stay zero, so every term of a diagonal sum below is a plain
@@ -395,11 +396,11 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
   __shared__ float Lq[kStepF], Dq[kStepF];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
-  const int nkb = (S + kRowsF - 1) / kRowsF;
+  // Key blocks [kb0, kb0 + nkc) of every (batch, head).
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int bh = tile / nkb, b = bh / H, h = bh - b * H;
-  const int kblk = tile - bh * nkb;
-  const int j_wg = kblk * kRowsF;
+  const int bh = tile / nkc, b = bh / H, h = bh - b * H;
+  const int kbl = tile - bh * nkc;
+  const int j_wg = (kb0 + kbl) * kRowsF;
   const int kk = wave * 32 + l32, kj = j_wg + kk;
   const bool kvalid = kj < S;
   const int ns = D >> 1;
@@ -410,7 +411,7 @@ __global__ __launch_bounds__(kThreadsF) void relpos_bwd_dkdv_f32_kernel(
   const float* pdh = pd + (int64_t)h * npd;
   const float* lse_bh = lse + (int64_t)bh * S;
   const float* dl_bh = delta_ws + (int64_t)bh * S;
-  float* prow = part + ((int64_t)bh * nkb + kblk) * (S + kRowsF);
+  float* prow = part + ((int64_t)bh * nkc + kbl) * (S + kRowsF);
   const int rlen = S + kRowsF - 1;  // diagonals of the partial row
 
   float kr[G::HM], vr[G::HM];
@@ -522,13 +523,19 @@ void launch_fwd_f32(const float* qkv, int64_t ld, const float* pd, float* out, f
 
 template <int DB>
 void launch_bwd_f32(const float* dout, const float* qkv, int64_t ld, const float* pd, const float* out32,
-                    const float* lse, float* dqkv, int64_t ldd, float* delta, float* part, int B, int S,
-                    int H, int D, float scale, hipStream_t st) {
-  const dim3 grid((unsigned)(ceil_div(S, kRowsF) * B * H));
-  hipLaunchKernelGGL((relpos_bwd_dq_f32_kernel<DB>), grid, dim3(kThreadsF), 0, st, qkv, ld, pd, dout, out32,
-                     lse, delta, dqkv, ldd, S, H, D, scale);
-  hipLaunchKernelGGL((relpos_bwd_dkdv_f32_kernel<DB>), grid, dim3(kThreadsF), 0, st, qkv, ld, pd, dout, lse,
-                     (const float*)delta, dqkv, ldd, part, S, H, D, scale);
+                    const float* lse, float* dqkv, int64_t ldd, float* dpd, float* delta, float* part,
+                    int nkc, int B, int S, int H, int D, float scale, hipStream_t st) {
+  const int nkb = (int)ceil_div(S, kRowsF);
+  hipLaunchKernelGGL((relpos_bwd_dq_f32_kernel<DB>), dim3((unsigned)(nkb * B * H)), dim3(kThreadsF), 0, st, qkv,
+                     ld, pd, dout, out32, lse, delta, dqkv, ldd, S, H, D, scale);
+  // Key blocks in chunks of nkc (all of them with the full workspace); each chunk's partial
+  // rows are summed into dpd before the next chunk overwrites them.
+  for (int kb0 = 0; kb0 < nkb; kb0 += nkc) {
+    const int n = min(nkc, nkb - kb0);
+    hipLaunchKernelGGL((relpos_bwd_dkdv_f32_kernel<DB>), dim3((unsigned)(n * B * H)), dim3(kThreadsF), 0, st,
+                       qkv, ld, pd, dout, lse, (const float*)delta, dqkv, ldd, part, S, H, D, scale, kb0, n);
+    launch_dpd_reduce(part, dpd, B, S, H, kb0, n, kb0 > 0, st);
+  }
 }
 
 }  // namespace
@@ -547,17 +554,17 @@ int relpos_fwd_f32(const float* qkv, int64_t ld, const float* pd, float* out, fl
 
 int relpos_bwd_f32(const float* dout, const float* qkv, int64_t ld, const float* pd, const float* out32,
                    const float* lse, float* dqkv, int64_t ldd, float* dpd, float* delta, float* part,
-                   int B, int S, int H, int D, float scale, hipStream_t st) {
+                   int nkc, int B, int S, int H, int D, float scale, hipStream_t st) {
+#define KRSI_BWD_F32(DB_) \
+  launch_bwd_f32<DB_>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, dpd, delta, part, nkc, B, S, H, D, scale, st)
   switch ((D + 31) / 32) {
-    case 1: launch_bwd_f32<1>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, delta, part, B, S, H, D, scale, st); break;
-    case 2: launch_bwd_f32<2>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, delta, part, B, S, H, D, scale, st); break;
-    case 3: launch_bwd_f32<3>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, delta, part, B, S, H, D, scale, st); break;
-    case 4: launch_bwd_f32<4>(dout, qkv, ld, pd, out32, lse, dqkv, ldd, delta, part, B, S, H, D, scale, st); break;
+    case 1: KRSI_BWD_F32(1); break;
+    case 2: KRSI_BWD_F32(2); break;
+    case 3: KRSI_BWD_F32(3); break;
+    case 4: KRSI_BWD_F32(4); break;
     default: return KRSI_ERR_UNSUPPORTED;
   }
-  const int rc = launch_status();
-  if (rc != KRSI_OK) return rc;
-  launch_dpd_reduce(part, dpd, B, S, H, st);
+#undef KRSI_BWD_F32
   return launch_status();
 }
 

@@ -22,9 +22,16 @@ __device__ __forceinline__ int xcd_tile(int w, int N) {
   return x * q + min(x, r) + k;
 }
 
-// dpd = sum over batches and key blocks of the dpd partial rows (fixed order), launched on
-// `stream` after the dK/dV kernel has written `part`. Defined in relpos_attn.hip.
-void launch_dpd_reduce(const float* part, float* dpd, int B, int S, int H, hipStream_t stream);
+// dpd (+)= sum over batches and key blocks kb0 .. kb0 + nkc - 1 of the dpd partial rows
+// (fixed order), launched on `stream` after the dK/dV kernel has written `part`, which holds
+// the rows of those nkc key blocks only. acc_in adds the sum to dpd instead of storing it.
+// Defined in relpos_attn.hip.
+void launch_dpd_reduce(const float* part, float* dpd, int B, int S, int H, int kb0, int nkc,
+                       bool acc_in, hipStream_t stream);
+
+// Key blocks whose partial rows fit a workspace of ws_bytes (delta first, then the rows),
+// at most all of them; 0 when not even one block's rows fit.
+int relpos_bwd_chunk_blocks(size_t ws_bytes, int B, int S, int H);
 
 // fp32 activations (relpos_attn_f32.hip). Arguments as the 16-bit entry points; the
 // caller has validated them.
@@ -32,7 +39,7 @@ int relpos_fwd_f32(const float* qkv, int64_t ld, const float* pd, float* out, fl
                    float* lse, int B, int S, int H, int D, float scale, hipStream_t st);
 int relpos_bwd_f32(const float* dout, const float* qkv, int64_t ld, const float* pd,
                    const float* out32, const float* lse, float* dqkv, int64_t ldd, float* dpd,
-                   float* delta, float* part, int B, int S, int H, int D, float scale,
+                   float* delta, float* part, int nkc, int B, int S, int H, int D, float scale,
                    hipStream_t st);
 
 }  // namespace krsi

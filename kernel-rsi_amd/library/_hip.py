@@ -10,13 +10,19 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_PATH = Path(__file__).resolve().parent.parent / "libkrsi_hip.so"
+# Cap in bytes on the attention backward's workspace (None: no cap, the fastest path). The
+# dpd partial rows grow as B H S^2 / 32 bytes; under a cap the backward takes the key blocks
+# in chunks (several dK/dV launches), never below one block's rows. Read from
+# KRSI_RELPOS_BWD_WORKSPACE_MAX at import; assignable.
+RELPOS_BWD_WORKSPACE_MAX: int | None = int(os.environ.get("KRSI_RELPOS_BWD_WORKSPACE_MAX", "0")) or None
 
 # Names and signatures of every entry point of include/krsi.h.
 _P, _I32, _I64, _F32, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
@@ -37,6 +43,7 @@ SIGNATURES = {
     "krsi_relpos_fwd": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _I32, _P]),
     "krsi_relpos_fwd_bf16": (ctypes.c_int, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32, _P]),
     "krsi_relpos_bwd_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "krsi_relpos_bwd_workspace_min_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "krsi_relpos_bwd": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _SZ,
                                        _I32, _I32, _I32, _I32, _F32, _I32, _P]),
     "krsi_relpos_bwd_bf16": (ctypes.c_int, [_P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _SZ,
@@ -100,6 +107,11 @@ def _rmsnorm_ws_bytes(rows: int, n: int) -> int:
 @functools.lru_cache(maxsize=256)
 def _relpos_ws_bytes(B: int, S: int, H: int, D: int) -> int:
     return lib().krsi_relpos_bwd_workspace_bytes(B, S, H, D)
+
+
+@functools.lru_cache(maxsize=256)
+def _relpos_ws_min_bytes(B: int, S: int, H: int, D: int) -> int:
+    return lib().krsi_relpos_bwd_workspace_min_bytes(B, S, H, D)
 
 
 def _on_gpu(*ts: torch.Tensor) -> None:
@@ -260,9 +272,12 @@ def relpos_fwd(qkv: torch.Tensor, pd: torch.Tensor, B: int, S: int, H: int, D: i
 
 
 def relpos_bwd(dout: torch.Tensor, qkv: torch.Tensor, pd: torch.Tensor, out32: torch.Tensor,
-               lse: torch.Tensor, B: int, S: int, H: int, D: int,
-               scale: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """dqkv (same shape and strides as a contiguous qkv) and dpd [H, 2S-1] fp32."""
+               lse: torch.Tensor, B: int, S: int, H: int, D: int, scale: float,
+               workspace_max: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """dqkv (same shape and strides as a contiguous qkv) and dpd [H, 2S-1] fp32.
+
+    workspace_max (default RELPOS_BWD_WORKSPACE_MAX) caps the workspace in bytes; it is
+    raised to the library's minimum (one key block's dpd partial rows) when below it."""
     dt = _check_relpos(qkv, pd, B, S, H, D)
     _on_gpu(dout, out32, lse)
     dout = dout.contiguous()
@@ -275,6 +290,9 @@ def relpos_bwd(dout: torch.Tensor, qkv: torch.Tensor, pd: torch.Tensor, out32: t
         dqkv[:, 3 * H * D:].zero_()
     dpd = torch.empty(H, 2 * S - 1, device=qkv.device, dtype=torch.float32)
     nbytes = _relpos_ws_bytes(B, S, H, D)
+    cap = RELPOS_BWD_WORKSPACE_MAX if workspace_max is None else workspace_max
+    if cap is not None and cap < nbytes:
+        nbytes = max(int(cap), _relpos_ws_min_bytes(B, S, H, D))
     ws = torch.empty(nbytes, device=qkv.device, dtype=torch.uint8)
     _check(lib().krsi_relpos_bwd(_ptr(dout), _ptr(qkv), qkv.stride(0), _ptr(pd), _ptr(out32),
                                  _ptr(lse), _ptr(dqkv), dqkv.stride(0), _ptr(dpd), _ptr(ws), nbytes,

@@ -56,6 +56,13 @@ def test_workspace_sizes():
     # delta [B,H,S] + one fp32 partial row of S+128 diagonals per 128-query block
     assert b >= 4 * 16 * 4096 * 4 + 4 * 16 * 32 * (4096 + 128) * 4
     assert lib.krsi_relpos_bwd_workspace_bytes(0, 4096, 16, 64) == 0
+    # The smallest workspace: delta and the partial rows of one 128-key block.
+    m = lib.krsi_relpos_bwd_workspace_min_bytes(4, 4096, 16, 64)
+    assert m == 4 * 16 * 4096 * 4 + 4 * 16 * (4096 + 128) * 4
+    assert lib.krsi_relpos_bwd_workspace_min_bytes(4, 4096, 0, 64) == 0
+    # One key block in all (S <= 128): the minimum is the full size up to its 256-byte padding.
+    full, low = lib.krsi_relpos_bwd_workspace_bytes(3, 100, 5, 64), lib.krsi_relpos_bwd_workspace_min_bytes(3, 100, 5, 64)
+    assert low <= full < low + 256
 
 
 def test_validation_before_launch():
@@ -98,7 +105,7 @@ def test_validation_before_launch():
     assert lib.krsi_relpos_fwd_bf16(FAKE, 384, FAKE, FAKE, FAKE, NULL, 2, 16, 2, 64, 0.125, NULL) == E["NULL"]
     assert lib.krsi_relpos_fwd_bf16(FAKE, 384, FAKE, FAKE, NULL, NULL, 2, 16, 0, 64, 0.125, NULL) == E["SHAPE"]
     assert fwd(B=40000, H=2) == E["SHAPE"]   # B*H above the grid limit
-    ws = lib.krsi_relpos_bwd_workspace_bytes(args["B"], args["S"], args["H"], args["D"])
+    ws = lib.krsi_relpos_bwd_workspace_min_bytes(args["B"], args["S"], args["H"], args["D"])
     assert lib.krsi_relpos_bwd_bf16(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 384, FAKE, FAKE, ws - 1,
                                     2, 16, 2, 64, 0.125, NULL) == E["WS"]
     assert lib.krsi_relpos_bwd_bf16(FAKE, FAKE, 384, FAKE, FAKE, FAKE, FAKE, 200, FAKE, FAKE, ws,

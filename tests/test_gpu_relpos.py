@@ -214,6 +214,44 @@ def test_relpos_backward_grid_paths(B, S, H):
     _check(B, S, H, 64, 0.125, ref_device="cuda")
 
 
+@pytest.mark.parametrize("B,S,H,D,dt,chunks", [
+    (1, 1101, 3, 64, torch.bfloat16, (1, 4)),   # 9 key blocks; S % 4 != 0: the scalar dpd sum
+    (2, 520, 2, 80, torch.float16, (2,)),       # 5 key blocks, D 80; the 128-bit dpd sum
+    (1, 700, 2, 64, torch.float32, (1, 4)),     # fp32 kernels
+    (1, 512, 4, 64, torch.bfloat16, (3,)),      # a grid that pairs dQ and dK/dV when unchunked
+])
+def test_relpos_backward_bounded_workspace(B, S, H, D, dt, chunks):
+    """A workspace that holds the dpd partial rows of only `c` of the ceil(S/128) key blocks
+    (down to krsi_relpos_bwd_workspace_min_bytes, c = 1): the key blocks go in chunks of c,
+    one dK/dV launch and one dpd sum each. dqkv is bitwise the full-workspace result (each
+    block's dK/dV does not depend on the chunking); dpd is the same terms summed in another
+    order, equal to fp32 rounding (rel 1e-5 of its largest entry)."""
+    qkv = seeded((B * S, 3 * H * D), 5, dtype=dt)
+    pd = seeded((H, 2 * S - 1), 6, std=0.02, dtype=torch.float32)
+    dout = seeded((B * S, H * D), 7, dtype=dt)
+    out, out32, lse = _hip.relpos_fwd(qkv, pd, B, S, H, D, 0.125)
+    full = _hip.relpos_bwd(dout, qkv, pd, out32, lse, B, S, H, D, 0.125)
+    lo = _hip.lib().krsi_relpos_bwd_workspace_min_bytes(B, S, H, D)
+    rows = B * H * (S + 128) * 4
+    for c in chunks:
+        log(f"relpos bounded workspace B{B} S{S} H{H} D{D} {dt}: {c} key blocks per launch")
+        dqkv, dpd = _hip.relpos_bwd(dout, qkv, pd, out32, lse, B, S, H, D, 0.125,
+                                    workspace_max=lo + (c - 1) * rows)
+        assert torch.equal(dqkv, full[0]), f"{c} blocks per launch"
+        torch.testing.assert_close(dpd, full[1], rtol=0, atol=1e-5 * full[1].abs().max().item())
+    # The cap is raised to the minimum, so a cap of 1 byte runs one block per launch.
+    dqkv, dpd = _hip.relpos_bwd(dout, qkv, pd, out32, lse, B, S, H, D, 0.125, workspace_max=1)
+    assert torch.equal(dqkv, full[0])
+
+
+def test_relpos_bounded_workspace_parity(monkeypatch):
+    """relpos_attention's backward under the module-wide workspace cap (one key block per
+    dK/dV launch) against the fp32 reference, to the parity bar of the unbounded path."""
+    monkeypatch.setattr(_hip, "RELPOS_BWD_WORKSPACE_MAX", 1)
+    log("relpos bounded workspace parity B2 S700 H2 D64")
+    _check(2, 700, 2, 64, 0.125)
+
+
 def test_relpos_backward_deterministic():
     log("relpos determinism B2 S512 H4 D64")
     B, S, H, D = 2, 512, 4, 64
