@@ -478,12 +478,14 @@ constexpr int kWaveTile = 32 * kStoreLd;  // floats per wave
 template <int DT, int DP, bool W32, typename Op>
 __device__ __forceinline__ void store_rows_staged(const f32x16* acc, Op op, int lane, int nrows, int64_t row0,
                                                   int64_t rstride, int D, uint16_t* __restrict__ out,
-                                                  float* __restrict__ out32, float* wt) {
+                                                  float* __restrict__ out32, float* wt, int db_lo = 0,
+                                                  int db_hi = Geo<DP>::DB) {
   const int g = lane >> 5, l32 = lane & 31;
 #pragma unroll
   for (int db = 0; db < Geo<DP>::DB; ++db) {
     const int ncol = min(32, D - 32 * db);  // a multiple of 8
     if (ncol <= 0) break;
+    if (db < db_lo || db >= db_hi) continue;  // wave-uniform
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       f32x4 o;
@@ -523,11 +525,12 @@ template <int DT, int DP>
 __device__ __forceinline__ void fwd_store_staged(const f32x16* oacc, float m_run, const float* l_run,
                                                  int lane, int nrows, int64_t row0, int64_t HD, int D,
                                                  uint16_t* __restrict__ out, float* __restrict__ out32,
-                                                 float* __restrict__ lse_q, float* wt) {
+                                                 float* __restrict__ lse_q, float* wt, int db_lo = 0,
+                                                 int db_hi = Geo<DP>::DB) {
   const float l = xhalf_sum(l_run[0] + l_run[1]);
   if (lse_q && (lane >> 5) == 0 && (lane & 31) < nrows) *lse_q = m_run + log2f(l);
   store_rows_staged<DT, DP, true>(oacc, [l](float x) { return x / l; }, lane, nrows, row0, HD, D, out, out32,
-                                  wt);
+                                  wt, db_lo, db_hi);
 }
 
 // At head dims 49-64 (DP = 64) the forward runs 4 waves per SIMD (128 VGPRs; spills only in the
@@ -752,37 +755,56 @@ __global__ __launch_bounds__(512, (!WIDE && (DP == 64 || DP <= 32) ? 4 : 2)) voi
     step(it, kBuf0, kTail);
   }
 
-  // Hand-over through the (now idle) tile buffers: per lane of group 1, m, l and the
-  // accumulators, at [wave-in-group][slot][lane] so every access is one coalesced row.
-  constexpr int SLOTS = 2 + 16 * G::DB;
-  static_assert(4 * SLOTS * 64 * 4 <= (int)sizeof(stage), "the hand-over fits the tile buffers");
+  // Hand-over through the (now idle) tile buffers, at [wave-in-group][slot][lane] so every
+  // access is one coalesced row. With more than one 32-column block the two groups split the
+  // merge and the store: group 0 takes blocks [0, DB0) and lse, group 1 blocks [DB0, DB), each
+  // handing the other its m, its l and the accumulator blocks the other stores. Both compute
+  // m = max(m0, m1), x = x0 2^(m0 - m) + x1 2^(m1 - m) with the same operations in the same
+  // order, so the outputs are those of a single merge.
+  constexpr int DB = G::DB;
+  constexpr int DB0 = DB > 1 ? (DB + 1) / 2 : DB;
+  constexpr int SENT = DB0 > DB - DB0 ? DB0 : DB - DB0;  // blocks one wave hands over, at most
+  constexpr int SLOTS = 2 + 16 * SENT;
+  static_assert((DB > 1 ? 8 : 4) * SLOTS * 64 * 4 <= (int)sizeof(stage), "the hand-over fits the tile buffers");
+  static_assert(32 * kStoreLd <= SLOTS * 64, "the staging tile fits a wave's hand-over rows");
+  // Group 1 writes region [gw] (read by group 0), group 0 region [4 + gw].
+  float* const sent = reinterpret_cast<float*>(stage) + ((grp == 1 ? 0 : 4) + gw) * SLOTS * 64 + lane;
+  float* const got = reinterpret_cast<float*>(stage) + ((grp == 1 ? 4 : 0) + gw) * SLOTS * 64 + lane;
   __syncthreads();
-  float* mine = reinterpret_cast<float*>(stage) + (gw * SLOTS) * 64 + lane;
-  if (grp == 1) {
-    mine[0] = m_run;
-    mine[64] = l_run[0] + l_run[1];
+  if (grp == 1 || DB > 1) {
+    const int lo = grp == 1 ? 0 : DB0, hi = grp == 1 ? DB0 : DB;  // blocks the other group stores
+    sent[0] = m_run;
+    sent[64] = l_run[0] + l_run[1];
 #pragma unroll
-    for (int db = 0; db < G::DB; ++db)
+    for (int db = 0; db < DB; ++db)
+      if (db >= lo && db < hi)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mine[(2 + 16 * db + r) * 64] = oacc[db][r];
+        for (int r = 0; r < 16; ++r) sent[(2 + 16 * (db - lo) + r) * 64] = oacc[db][r];
   }
   __syncthreads();
-  if (grp == 0) {
-    const float m1 = mine[0], l1 = mine[64];
-    const float m = fmaxf(m_run, m1);
-    const float a0 = __builtin_amdgcn_exp2f(m_run - m);
+  if (grp == 0 || DB > 1) {
+    const int lo = grp == 0 ? 0 : DB0, hi = grp == 0 ? DB0 : DB;  // blocks this group stores
+    const float mo = got[0], lo_l = got[64];
+    const float m0 = grp == 0 ? m_run : mo, m1 = grp == 0 ? mo : m_run;
+    const float l0 = grp == 0 ? l_run[0] + l_run[1] : lo_l, l1 = grp == 0 ? lo_l : l_run[0] + l_run[1];
+    const float m = fmaxf(m0, m1);
+    const float a0 = __builtin_amdgcn_exp2f(m0 - m);
     const float a1 = __builtin_amdgcn_exp2f(m1 - m);  // 0 when group 1 saw no finite score
-    const float lm[2] = {(l_run[0] + l_run[1]) * a0 + l1 * a1, 0.f};
+    const float lm[2] = {l0 * a0 + l1 * a1, 0.f};
 #pragma unroll
-    for (int db = 0; db < G::DB; ++db)
+    for (int db = 0; db < DB; ++db)
+      if (db >= lo && db < hi)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] = oacc[db][r] * a0 + mine[(2 + 16 * db + r) * 64] * a1;
-    // The wave's hand-over rows, all read above, become its output staging tile.
-    static_assert(32 * kStoreLd <= SLOTS * 64, "the staging tile fits a wave's hand-over rows");
+        for (int r = 0; r < 16; ++r) {
+          const float xo = got[(2 + 16 * (db - lo) + r) * 64];
+          const float x0 = grp == 0 ? oacc[db][r] : xo, x1 = grp == 0 ? xo : oacc[db][r];
+          oacc[db][r] = x0 * a0 + x1 * a1;
+        }
+    // The wave's received rows, all read above, become its output staging tile.
     asm volatile("" ::: "memory");
     fwd_store_staged<DT, DP>(oacc, m, lm, lane, min(32, S - (i_wg + gw * 32)),
                              (tok0 + i_wg + gw * 32) * HD + (int64_t)h * D, HD, D, out, out32,
-                             (lse ? lse + (int64_t)bh * S + qi : nullptr), reinterpret_cast<float*>(stage) + (gw * SLOTS) * 64);
+                             (lse && grp == 0 ? lse + (int64_t)bh * S + qi : nullptr), got - lane, lo, hi);
   }
 }
 
