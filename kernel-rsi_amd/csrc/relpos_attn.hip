@@ -1410,10 +1410,15 @@ __global__ __launch_bounds__(256, (DP <= 64 ? 2 : 1)) void relpos_bwd_pair_kerne
     kind = k >= half;
     idx = x * half + k - kind * half;
   }
-  if (kind)
+  // The dK/dV blocks carry about 1.7x the dQ blocks' work, so they set the launch's length: their
+  // waves issue ahead of the dQ waves sharing their SIMDs (outputs bitwise the same; backward,
+  // interleaved A/B: B4 S512 H16 D64 39.4 -> 36.5 us, B2 S1024 H16 57.1 -> 52.2, B1 S2048 H16
+  // 92.8 -> 87.1; priority 3, or the dQ waves lowered instead, measured the same).
+  if (kind) {
+    __builtin_amdgcn_s_setprio(1);
     bwd_dkdv_body<DT, DP, 4>(idx, lds, qkv, ld, pd, dout, lse, delta_ws, dqkv, ldd, part, S, H, D, f, scale, 0,
                              (S + 127) / 128);
-  else
+  } else
     bwd_dq_body<DT, DP, 4, true>(idx, lds, qkv, ld, pd, dout, out32, lse, delta_ws, dqkv, ldd, S, H, D, f,
                                  scale);
 }
