@@ -22,7 +22,18 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "libkrsi_hip.so"
 # dpd partial rows grow as B H S^2 / 32 bytes; under a cap the backward takes the key blocks
 # in chunks (several dK/dV launches), never below one block's rows. Read from
 # KRSI_RELPOS_BWD_WORKSPACE_MAX at import; assignable.
-RELPOS_BWD_WORKSPACE_MAX: int | None = int(os.environ.get("KRSI_RELPOS_BWD_WORKSPACE_MAX", "0")) or None
+def _env_bytes(name: str) -> int | None:
+    raw = os.environ.get(name, "").strip()
+    if not raw:
+        return None
+    try:
+        v = int(raw)
+    except ValueError:
+        raise ValueError(f"{name}={raw!r}: expected a byte count (integer)") from None
+    return v if v > 0 else None
+
+
+RELPOS_BWD_WORKSPACE_MAX: int | None = _env_bytes("KRSI_RELPOS_BWD_WORKSPACE_MAX")
 
 # Names and signatures of every entry point of include/krsi.h.
 _P, _I32, _I64, _F32, _SZ = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t

@@ -233,3 +233,14 @@ def test_modules_keep_the_reference_interface():
         ["qkv", "pd", "B", "S", "H", "D", "scale"]
     for m in (rmsnorm, geglu, relpos_attention):
         assert callable(m.selftest) and callable(m.reference)
+
+
+def test_workspace_cap_from_environment(monkeypatch):
+    """KRSI_RELPOS_BWD_WORKSPACE_MAX: unset, empty or <= 0 means no cap; a non-integer is
+    refused with the variable's name in the message."""
+    for raw, want in (("", None), ("0", None), ("-5", None), (" 4096 ", 4096)):
+        monkeypatch.setenv("KRSI_RELPOS_BWD_WORKSPACE_MAX", raw)
+        assert _hip._env_bytes("KRSI_RELPOS_BWD_WORKSPACE_MAX") == want
+    monkeypatch.setenv("KRSI_RELPOS_BWD_WORKSPACE_MAX", "64MB")
+    with pytest.raises(ValueError, match="KRSI_RELPOS_BWD_WORKSPACE_MAX"):
+        _hip._env_bytes("KRSI_RELPOS_BWD_WORKSPACE_MAX")
