@@ -219,6 +219,7 @@ def test_relpos_backward_grid_paths(B, S, H):
     (2, 520, 2, 80, torch.float16, (2,)),       # 5 key blocks, D 80; the 128-bit dpd sum
     (1, 700, 2, 64, torch.float32, (1, 4)),     # fp32 kernels
     (1, 512, 4, 64, torch.bfloat16, (3,)),      # a grid that pairs dQ and dK/dV when unchunked
+    (1, 777, 2, 128, torch.bfloat16, (2,)),     # D 128 (one wave per SIMD); chunks 2, 2, 2, 1
 ])
 def test_relpos_backward_bounded_workspace(B, S, H, D, dt, chunks):
     """A workspace that holds the dpd partial rows of only `c` of the ceil(S/128) key blocks
@@ -288,6 +289,34 @@ def test_relpos_graph_replay_matches_eager():
     equals the eager result (the kernels use no memset and keep no state between calls)."""
     log("relpos graph replay B1 S256 H2 D64")
     B, S, H, D = 1, 256, 2, 64
+    qkv, pd, dout = _inputs(B, S, H, D)
+    eager = _kernel(qkv, pd, dout, B, S, H, D, 0.125)
+    x = qkv.detach().requires_grad_(True)
+    p = pd.detach().requires_grad_(True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            torch.autograd.grad(A.relpos_attention(x, p, B, S, H, D, 0.125), [x, p], dout)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = A.relpos_attention(x, p, B, S, H, D, 0.125)
+        dq, dp = torch.autograd.grad(out, [x, p], dout)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[0]) and torch.equal(dq, eager[1]) and torch.equal(dp, eager[2])
+        _kernel(qkv, pd, dout, B, S, H, D, 0.5)   # unrelated eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_relpos_graph_replay_bounded_workspace(monkeypatch):
+    """The chunked backward (one dK/dV launch and one accumulating dpd sum per key block)
+    captured in a HIP graph: every replay equals the eager result, with eager work between."""
+    monkeypatch.setattr(_hip, "RELPOS_BWD_WORKSPACE_MAX", 1)
+    log("relpos graph replay, bounded workspace, B1 S600 H2 D64")
+    B, S, H, D = 1, 600, 2, 64
     qkv, pd, dout = _inputs(B, S, H, D)
     eager = _kernel(qkv, pd, dout, B, S, H, D, 0.125)
     x = qkv.detach().requires_grad_(True)
